@@ -1,0 +1,286 @@
+"""Benchmark of the MI355X verify/draft hot path.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+
+Headline (the `value`): the fused RMSNorm -> linear with fp8-e4m3 weights
+and per-channel fp32 scales, x bf16 [64, 4096] (a 64-node verify tree),
+W [14336, 4096], gamma, bf16 out — algorithmic GB/s of one launch. A step is
+one launch; weights rotate over enough copies that no launch reads W from
+the 256 MB Infinity Cache. Launches go straight through the C ABI with
+preallocated outputs on torch's current stream, timed with HIP events on
+that stream. --all also measures the other workloads (fp32 linear, fp8 at
+M = 8 / 32, multi-verify chain, INT4 linear) into "detail".
+
+Prints ONE JSON line. The CPU baseline times the oracle's eager restatement
+of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "mtp-engine_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 * 2 ** 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def rotations(weight_bytes: int) -> int:
+    return max(2, -(-512 * 2 ** 20 // max(1, weight_bytes)) + 1)
+
+
+class Case:
+    """A workload bound to preallocated device buffers; launch(i) enqueues
+    one kernel launch on rotation i."""
+
+    def __init__(self, name, launch, nbytes, flops, bound, nrot):
+        self.name, self.launch, self.nbytes, self.flops = name, launch, nbytes, flops
+        self.bound, self.nrot = bound, nrot
+
+
+def time_case(torch, case: Case, steps: int, warmup: int):
+    for i in range(warmup):
+        case.launch(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(st)
+    for i in range(steps):
+        case.launch(i)
+    t1.record(st)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1)
+    return ms / steps
+
+
+def make_fp8_case(torch, lib, L, M: int):
+    from mtp_hip import workloads
+    d = workloads.fp8_linear(M)
+    dev = torch.device("cuda")
+    N, K = d["weight_fp8"].shape
+    wbytes = N * K
+    nrot = rotations(wbytes + N * 4)
+    ws_list = [d["weight_fp8"].to(dev) for _ in range(nrot)]
+    sc_list = [d["wscale"].to(dev) for _ in range(nrot)]
+    x = d["x"].to(dev)
+    gamma = d["gamma"].to(dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    nws = lib.mtp_rmsnorm_linear_workspace_bytes(L.BF16, L.FP8E4M3, M, N, K)
+    ws = torch.zeros(max(nws, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.mtp_fused_rmsnorm_linear_fp8
+    args = [(x.data_ptr(), L.BF16, M, K, w.data_ptr(), L.FP8E4M3, s.data_ptr(), N, None, 0,
+             gamma.data_ptr(), L.F32, ctypes.c_float(d["eps"]), 1, y.data_ptr(), ws.data_ptr(),
+             nws, stream) for w, s in zip(ws_list, sc_list)]
+
+    def launch(i):
+        st = fn(*args[i % nrot])
+        if st != 0:
+            raise RuntimeError(f"fp8 launch failed: {st}")
+
+    nbytes = M * K * 2 + N * K + N * 4 + K * 4 + M * N * 2
+    flops = 2 * M * N * K
+    case = Case(f"fp8_rmsnorm_linear_M{M}", launch, nbytes, flops, "hbm", nrot)
+    case.keep = (ws_list, sc_list, x, gamma, y, ws, d)
+    return case
+
+
+def make_fp32_case(torch, lib, L):
+    from mtp_hip import workloads
+    d = workloads.fp32_linear()
+    dev = torch.device("cuda")
+    M, K = d["x"].shape
+    N = d["weight"].shape[0]
+    nrot = rotations(N * K * 4)
+    wl = [d["weight"].to(dev) for _ in range(nrot)]
+    x, gamma = d["x"].to(dev), d["gamma"].to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    nws = lib.mtp_rmsnorm_linear_workspace_bytes(L.F32, L.F32, M, N, K)
+    ws = torch.zeros(max(nws, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.mtp_fused_rmsnorm_linear
+    args = [(x.data_ptr(), L.F32, M, K, w.data_ptr(), L.F32, N, None, 0, gamma.data_ptr(), L.F32,
+             ctypes.c_float(d["eps"]), ctypes.c_float(1.0), 1, y.data_ptr(), ws.data_ptr(), nws,
+             stream) for w in wl]
+
+    def launch(i):
+        st = fn(*args[i % nrot])
+        if st != 0:
+            raise RuntimeError(f"fp32 launch failed: {st}")
+
+    nbytes = M * K * 4 + N * K * 4 + K * 4 + M * N * 4
+    case = Case("fp32_rmsnorm_linear_M16", launch, nbytes, 2 * M * N * K, "hbm", nrot)
+    case.keep = (wl, x, gamma, y, ws)
+    return case
+
+
+def make_verify_case(torch, lib, L):
+    import torch.nn.functional as F
+    from mtp_hip import workloads
+    d = workloads.multi_verify()
+    dev = torch.device("cuda")
+    hidden = d["hidden"].to(dev)
+    W = d["weight"].to(dev)
+    B, S, K = hidden.shape
+    V = W.shape[0]
+    D = S - 1
+    # drafts from the target argmax (synthetic input construction only)
+    with torch.no_grad():
+        Wf = W.float().contiguous()
+        top = F.linear(hidden.reshape(-1, K).float(), Wf).argmax(-1)
+        del Wf
+    draft = workloads.make_chain_drafts(top.reshape(B, S).cpu(), V, d["seed"]).to(dev)
+    draft32 = draft.to(torch.int32)
+    accept = torch.empty((B, D), dtype=torch.int8, device=dev)
+    acc_n = torch.empty((B,), dtype=torch.int32, device=dev)
+    corr = torch.empty((B,), dtype=torch.int32, device=dev)
+    nws = lib.mtp_verify_workspace_bytes(L.BF16, B * S, S, V, K)
+    ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.mtp_fused_multi_verify
+    args = (hidden.data_ptr(), L.BF16, B, S, K, W.data_ptr(), L.BF16, V, None, 0,
+            draft32.data_ptr(), D, accept.data_ptr(), acc_n.data_ptr(), corr.data_ptr(), None,
+            ws.data_ptr(), nws, stream)
+
+    def launch(i):
+        st = fn(*args)
+        if st != 0:
+            raise RuntimeError(f"multi-verify launch failed: {st}")
+
+    nbytes = B * S * K * 2 + V * K * 2 + B * D * 4 + B * D + B * 4 * 2
+    case = Case("multi_verify_B8_S5_V128256", launch, nbytes, 2 * B * S * K * V, "hbm", 1)
+    case.keep = (hidden, W, draft32, accept, acc_n, corr, ws)
+    return case
+
+
+def cpu_baseline_fp8(torch, M: int):
+    from mtp_hip import workloads
+    from oracle import eager as O
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    d = workloads.fp8_linear(M)
+    fn = lambda: O.rmsnorm_linear_fp8(d["x"], d["weight_fp8"], d["wscale"], None, d["eps"],
+                                      gamma=d["gamma"])
+    fn()
+    times = []
+    t_end = time.time() + 10.0
+    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    N, K = d["weight_fp8"].shape
+    nbytes = M * K * 2 + N * K + N * 4 + K * 4 + M * N * 2
+    med = statistics.median(times)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(),
+                kind="port",
+                sample=f"full workload (M={M}), median of {len(times)} runs, "
+                       f"{med * 1e3:.1f} ms/run; eager fp32 restatement (fp8 decode + F.linear); "
+                       f"{cpu_model}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--all", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs on a single MI355X and has no "
+              "multi-GPU path (see DESIGN.md for how the path would shard).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mtp_hip import _lib as L
+    lib = L.load()
+    assert torch.cuda.is_available(), "bench.py needs a HIP GPU"
+
+    detail = {}
+    headline = None
+    builders = [("fp8_M64", lambda: make_fp8_case(torch, lib, L, 64))]
+    if args.all:
+        builders += [("fp8_M8", lambda: make_fp8_case(torch, lib, L, 8)),
+                     ("fp8_M32", lambda: make_fp8_case(torch, lib, L, 32)),
+                     ("fp32_M16", lambda: make_fp32_case(torch, lib, L)),
+                     ("multi_verify", lambda: make_verify_case(torch, lib, L))]
+    if args.only:
+        builders = [b for b in builders if b[0] in args.only.split(",")]
+    for key, mk in builders:
+        log(f"[bench] building {key}")
+        case = mk()
+        steps = args.steps if case.nbytes < 2e8 else max(10, args.steps // 10)
+        ms = time_case(torch, case, steps, args.warmup)
+        us = ms * 1e3
+        gbs = case.nbytes / (ms * 1e-3) / 1e9
+        tfl = case.flops / (ms * 1e-3) / 1e12
+        detail[key] = dict(workload=case.name, us_per_launch=round(us, 3), GBps=round(gbs, 1),
+                           TFLOPs=round(tfl, 2), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                           mfma_frac=round(tfl / BF16_MFMA_PEAK_TFLOPS, 4),
+                           algorithmic_bytes=case.nbytes, flops=case.flops,
+                           weight_rotations=case.nrot, steps=steps)
+        log(f"[bench] {key}: {us:.2f} us  {gbs:.0f} GB/s  {tfl:.1f} TFLOP/s")
+        if key == "fp8_M64":
+            headline = (case, ms, steps)
+        del case
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline (oracle, fp8 M=64)")
+        cpu = cpu_baseline_fp8(torch, 64)
+
+    case, ms, steps = headline
+    gbs = case.nbytes / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "fused RMSNorm+linear TFLOP/s & GB/s (% roofline); verify-step us, 1 GPU",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3-weights/bf16-act/fp32-acc",
+        "data": "synthetic (seeded torch CPU generator, weights rotated x%d past the 256 MB MALL)"
+                % case.nrot,
+        "config": {"workload": "fused RMSNorm+linear, fp8-e4m3 weights with per-channel fp32 "
+                               "scales: x bf16 [64,4096], gamma [4096], W [14336,4096], bf16 out",
+                   "M": 64, "K": 4096, "N": 14336, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": case.nbytes},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,189 @@
+/*
+ * mtp_hip.h — C ABI of the MI355X (gfx950) verify/draft hot path.
+ *
+ * One entry point per Python function of the reference's kernel layer.
+ * Every entry point:
+ *   - takes plain device pointers, element counts and dtype codes (no torch
+ *     types), all tensors contiguous row-major in the reference's layout
+ *     (nn.Linear weights are [N, K] = [out, in]);
+ *   - enqueues its kernels on `stream` (a hipStream_t; NULL = the null
+ *     stream) and returns without synchronising, so it can be captured into
+ *     a hipGraph;
+ *   - never allocates device memory: scratch comes from the caller through
+ *     `workspace` / `workspace_bytes`, sized by the matching *_workspace_bytes
+ *     query. The first MTP_WORKSPACE_COUNTER_BYTES of every workspace hold
+ *     arrival counters: they must be zero before the first use, and every
+ *     launch leaves the counters it used at zero again, so one workspace can
+ *     serve any sequence of calls (any entry point, any shape) on one stream
+ *     (calls that overlap on different streams need distinct workspaces);
+ *   - validates its arguments on the host before any HIP call and returns a
+ *     status code (MTP_OK = 0, negative on error; mtp_status_string() names
+ *     it). It never aborts the process.
+ */
+#ifndef MTP_HIP_H
+#define MTP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTP_ABI_VERSION 1
+
+/* Bytes at the start of a workspace reserved for arrival counters. */
+#define MTP_WORKSPACE_COUNTER_BYTES 65536
+
+/* Element type codes. */
+enum mtp_dtype {
+  MTP_F32 = 0,
+  MTP_BF16 = 1,
+  MTP_F16 = 2,
+  MTP_FP8E4M3 = 3, /* OCP float8_e4m3fn (torch.float8_e4m3fn) */
+  MTP_U8 = 4,
+  MTP_I8 = 5,
+  MTP_I32 = 6,
+  MTP_I64 = 7
+};
+
+/* Status codes. */
+enum mtp_status {
+  MTP_OK = 0,
+  MTP_ERR_NULL = -1,      /* a required pointer is NULL */
+  MTP_ERR_SHAPE = -2,     /* sizes inconsistent or out of the supported range */
+  MTP_ERR_DTYPE = -3,     /* unsupported dtype or dtype combination */
+  MTP_ERR_WORKSPACE = -4, /* workspace missing or smaller than required */
+  MTP_ERR_ALIGN = -5,     /* a pointer is not aligned as the kernel requires */
+  MTP_ERR_LAUNCH = -6,    /* the HIP runtime rejected a launch */
+  MTP_ERR_ARG = -7        /* any other invalid argument */
+};
+
+/* INT4 nibble conventions for mtp_fused_int4_matmul. */
+enum mtp_nibble {
+  /* nibble n decodes to n - 8: the reference decoder (mtp_kernels.py:758-762,
+   * 470-473); this is the parity contract. */
+  MTP_NIBBLE_OFFSET8 = 0,
+  /* nibble n is a two's-complement int4 (n >= 8 means n - 16): what the
+   * reference quantizer writes (mtp_kernels.py:742-750). */
+  MTP_NIBBLE_TWOS = 1
+};
+
+int mtp_abi_version(void);
+const char *mtp_status_string(int status);
+/* Name of the last HIP error seen by a failed launch on this thread. */
+const char *mtp_last_hip_error(void);
+
+/* ------------------------------------------------------------------------- */
+/* RMSNorm -> linear family                                                  */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Replaces fused_rmsnorm_linear(x, weight, bias=None, eps=1e-6, scale=None)
+ * (mtp_kernels.py:936-977; eager twin _eager_rmsnorm_linear 778-787):
+ *   y = cast_xdtype(((x * rsqrt(mean(x^2) + eps) * gamma) @ W^T + bias) * scale)
+ * x [M, K] in x_dtype (F32, BF16, F16); weight [N, K] in w_dtype (must equal
+ * x_dtype); bias [N] in bias_dtype or NULL (the reference casts bias to
+ * x.dtype first, mtp_kernels.py:952: the caller passes it already cast);
+ * gamma [K] in gamma_dtype or NULL (keyword extension; NULL = the reference);
+ * norm = 0 skips the RMSNorm (the no-norm mode CachedLinear needs,
+ * mtp_perf_hardening.py:150-165); y [M, N] in x_dtype.
+ * Arithmetic: products exact, fp32 accumulation (TF32 off for F32).
+ */
+int mtp_fused_rmsnorm_linear(const void *x, int x_dtype, int64_t M, int64_t K,
+                             const void *weight, int w_dtype, int64_t N,
+                             const void *bias, int bias_dtype,
+                             const void *gamma, int gamma_dtype, float eps,
+                             float scale, int norm, void *y, void *workspace,
+                             size_t workspace_bytes, void *stream);
+
+/*
+ * Replaces fused_rmsnorm_linear_fp8(x, weight_fp8, wscale, bias=None,
+ * eps=1e-6) (mtp_kernels.py:1014-1044; eager 804-814):
+ *   y = cast_xdtype((x * rstd * gamma) @ (fp8_to_f32(W) * wscale[:, None])^T + bias)
+ * weight_fp8 [N, K] in w_dtype: MTP_FP8E4M3 (float8_e4m3fn), or a float
+ * dtype (the reference accepts any weight dtype here; its self-test passes
+ * fp32 values in +-448, mtp_engine.py:1792-1800); wscale [N] fp32 (per output
+ * channel, a slice of the packed scale buffer of pack_scales,
+ * mtp_kernels.py:1336-1353).
+ */
+int mtp_fused_rmsnorm_linear_fp8(const void *x, int x_dtype, int64_t M,
+                                 int64_t K, const void *weight_fp8,
+                                 int w_dtype, const float *wscale, int64_t N,
+                                 const void *bias, int bias_dtype,
+                                 const void *gamma, int gamma_dtype, float eps,
+                                 int norm, void *y, void *workspace,
+                                 size_t workspace_bytes, void *stream);
+
+/*
+ * Replaces fused_int4_matmul(x, packed, scales, K, group=32)
+ * (mtp_kernels.py:1194-1219; eager 875-878; decoder 754-768):
+ *   y = cast_xdtype(xn @ Wdq^T),  Wdq[n, k] = nib(n, k) * scales[n, k / group]
+ * nib(n, k) is nibble (k & 1) of packed[n, k / 2] (low nibble for even k),
+ * decoded per `nibble` (MTP_NIBBLE_OFFSET8 = the reference). packed [N, K/2]
+ * u8; scales [N, ceil(K/group)] in scale_dtype (F32 or F16).
+ * norm = 0 is the reference (xn = x, no RMSNorm, G2); norm = 1 composes the
+ * RMSNorm prologue xn = x * rstd * gamma (the INT4 RMSNorm+linear workload).
+ */
+int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K,
+                          const uint8_t *packed, const void *scales,
+                          int scale_dtype, int64_t N, int64_t group,
+                          int nibble, const void *gamma, int gamma_dtype,
+                          float eps, int norm, void *y, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+/* Workspace bytes the three entry points above need for these sizes
+ * (w_kind: MTP_F32/MTP_BF16/MTP_F16 weights, MTP_FP8E4M3, or MTP_U8 for
+ * packed INT4). */
+size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M,
+                                          int64_t N, int64_t K);
+
+/* ------------------------------------------------------------------------- */
+/* Verify: lm_head GEMM -> argmax -> acceptance -> rollback index            */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Replaces fused_verify(hidden, weight, draft, bias=None) -> (accept, top)
+ * (mtp_fused_verify.py:199-234; kernel 42-80; eager 159-166):
+ *   top[m] = argmax_v(hidden[m] . W[v] + bias[v])  (lowest index on ties,
+ *            NaN counts as the maximum, as torch.argmax)
+ *   accept[m] = (top[m] == draft[m])
+ * hidden [M, K] (F32/BF16/F16), weight [V, K] same dtype, bias [V] or NULL,
+ * draft [M] int32 -> accept [M] int8, top [M] int32. Logits never reach HBM.
+ */
+int mtp_fused_verify(const void *hidden, int h_dtype, int64_t M, int64_t K,
+                     const void *weight, int w_dtype, int64_t V,
+                     const void *bias, int bias_dtype, const int32_t *draft,
+                     int8_t *accept, int32_t *top, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/*
+ * Replaces fused_multi_verify(hidden, weight, draft, bias=None)
+ *   -> (accept, accepted_n, corrected)
+ * (mtp_fused_verify.py:237-290; kernel 88-156; eager 169-196):
+ *   top[b, s] = argmax_v(hidden[b, s] . W[v] + bias[v]),  s = 0..D
+ *   accept[b, d] = (top[b, d+1] == draft[b, d]) and accept[b, d-1]
+ *   accepted_n[b] = number of leading accepted drafts (the rollback index)
+ *   corrected[b] = top[b, 0]
+ * hidden [B, S, K] with S == D + 1, weight [V, K], draft [B, D] int32.
+ * top_out [B, S] int32 may be NULL (keyword extension return_top).
+ */
+int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B,
+                           int64_t S, int64_t K, const void *weight,
+                           int w_dtype, int64_t V, const void *bias,
+                           int bias_dtype, const int32_t *draft, int64_t D,
+                           int8_t *accept, int32_t *accepted_n,
+                           int32_t *corrected, int32_t *top_out,
+                           void *workspace, size_t workspace_bytes,
+                           void *stream);
+
+/* Workspace bytes for mtp_fused_verify (rows = M, seq = 1) or
+ * mtp_fused_multi_verify (rows = B * S, seq = S) at vocabulary size V. */
+size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq,
+                                  int64_t V, int64_t K);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTP_HIP_H */

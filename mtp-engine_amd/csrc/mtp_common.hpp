@@ -1,0 +1,151 @@
+// Shared device helpers for the gfx950 kernels: vector types, dtype
+// conversions, MFMA wrappers and the argmax ordering torch uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mtp_hip.h"
+
+namespace mtp {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
+constexpr int kWave = 64;
+
+__host__ __device__ constexpr int dtype_bytes(int dt) {
+  return dt == MTP_F32 ? 4
+       : dt == MTP_BF16 ? 2
+       : dt == MTP_F16 ? 2
+       : dt == MTP_FP8E4M3 ? 1
+       : dt == MTP_U8 ? 1
+       : dt == MTP_I8 ? 1
+       : dt == MTP_I32 ? 4
+       : dt == MTP_I64 ? 8 : 0;
+}
+
+// ---- scalar conversions ---------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  _Float16 h;
+  uint16_t b = (uint16_t)bits16;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// Load element i of a tensor of dtype dt (F32/BF16/F16) as fp32.
+__device__ __forceinline__ float load_as_f32(const void *p, int dt, int64_t i) {
+  if (dt == MTP_F32) return ((const float *)p)[i];
+  uint32_t b = ((const uint16_t *)p)[i];
+  return dt == MTP_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// Round fp32 to the storage dtype (round-to-nearest-even, as torch's .to()).
+__device__ __forceinline__ void store_from_f32(void *p, int dt, int64_t i, float v) {
+  if (dt == MTP_F32) {
+    ((float *)p)[i] = v;
+  } else if (dt == MTP_BF16) {
+    __bf16 h = (__bf16)v;
+    ((__bf16 *)p)[i] = h;
+  } else {
+    _Float16 h = (_Float16)v;
+    ((_Float16 *)p)[i] = h;
+  }
+}
+
+// Pack two fp32 into two 16-bit floats of type CT (BF16 or F16), RNE.
+template <int CT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (CT == MTP_BF16) {
+    bf16x2 r;
+    r[0] = (__bf16)a;
+    r[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, r);
+  } else {
+    f16x2 r;
+    r[0] = (_Float16)a;
+    r[1] = (_Float16)b;
+    return __builtin_bit_cast(uint32_t, r);
+  }
+}
+
+// Unpack a dword holding two 16-bit floats of type DT into fp32.
+template <int DT>
+__device__ __forceinline__ f32x2 unpack2(uint32_t w) {
+  f32x2 r;
+  if constexpr (DT == MTP_BF16) {
+    r[0] = __uint_as_float(w << 16);
+    r[1] = __uint_as_float(w & 0xffff0000u);
+  } else {
+    r[0] = f16_bits_to_f32(w & 0xffffu);
+    r[1] = f16_bits_to_f32(w >> 16);
+  }
+  return r;
+}
+
+// Two fp8 e4m3fn values (the 16-bit half `hi` of w) -> two 16-bit floats of
+// type CT, exact (every e4m3fn value is representable in bf16 and f16).
+template <int CT, bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_ct(uint32_t w) {
+  if constexpr (CT == MTP_BF16) {
+    return __builtin_bit_cast(uint32_t,
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  } else {
+    return __builtin_bit_cast(uint32_t,
+                              __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+}
+
+__device__ __forceinline__ f32x2 fp8x2_to_f32(uint32_t w, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true)
+            : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+}
+
+// ---- MFMA ------------------------------------------------------------------
+// 16x16 output tile, fp32 accumulate. Operand lane layout (wave64):
+//   A (16 x Kstep): lane l holds row (l % 16), k-slots 8*(l/16) .. +7
+//   B (Kstep x 16): lane l holds col (l % 16), k-slots 8*(l/16) .. +7
+//   D (16 x 16):    lane l holds col (l % 16), rows 4*(l/16) .. +3
+// (for the f32 variant, Kstep = 4 and each lane holds one k-slot, l / 16).
+
+template <int CT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (CT == MTP_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---- argmax ordering (torch.argmax) ---------------------------------------
+// NaN is the maximum; among equal values (or among NaNs) the lower index wins.
+__device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+// ---- memory ---------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld_nt16(const void *p) {
+  return __builtin_nontemporal_load((const u32x4 *)p);
+}
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+
+}  // namespace mtp

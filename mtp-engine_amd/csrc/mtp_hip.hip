@@ -1,0 +1,358 @@
+// C ABI of the gfx950 verify/draft hot path: argument validation, launch
+// planning and kernel dispatch. Declarations and the reference interface
+// each entry point replaces are in include/mtp_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+
+#include "generic.hpp"
+#include "ws_dispatch.hpp"
+
+using namespace mtp;
+
+namespace {
+
+thread_local char g_last_hip_error[256] = "";
+
+int launch_status() {
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return MTP_OK;
+  std::strncpy(g_last_hip_error, hipGetErrorString(e), sizeof(g_last_hip_error) - 1);
+  return MTP_ERR_LAUNCH;
+}
+
+bool is_float_dt(int dt) { return dt == MTP_F32 || dt == MTP_BF16 || dt == MTP_F16; }
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Tuning override for sweeps: MTP_WS_TUNE="variant,splits" (-1 = default).
+void tune_override(int &variant, int &splits) {
+  const char *s = std::getenv("MTP_WS_TUNE");
+  if (!s || !*s) return;
+  int v = -1, sp = -1;
+  if (std::sscanf(s, "%d,%d", &v, &sp) >= 1) {
+    if (v >= 0) variant = v;
+    if (sp > 0) splits = sp;
+  }
+}
+
+typedef WsVariant Variant;
+int num_variants(int ct) { return ws_num_variants(ct); }
+Variant get_variant(int ct, int wt, int v) { return ws_variant(ct, wt, v); }
+WsKernel pick_kernel(int ct, int wt, int mt, int v, int epi) {
+  return ws_pick_kernel(ct, wt, mt, v, epi);
+}
+
+bool fast_pair(int ct, int wt) {
+  if (!is_float_dt(ct)) return false;
+  return wt == ct || wt == MTP_FP8E4M3;
+}
+
+constexpr int kTargetBlocks = 512;  // 2 workgroups per CU on 256 CUs
+constexpr size_t kCounterBytes = MTP_WORKSPACE_COUNTER_BYTES;
+constexpr int64_t kCounterSlots = (int64_t)(kCounterBytes / 4);
+
+struct Plan {
+  bool generic = true;
+  int ct = 0, wt = 0, mt = 0, variant = 0;
+  Variant var{};
+  int NG = 0, KB = 0, G = 0, S = 1, kb_per = 0, nkb = 0;
+  int rows_per_chunk = 64, chunks = 0, xcd_map = 0;
+  size_t part_off = 0, sqp_off = 0, ticket_off = 0, aval_off = 0, aidx_off = 0, total = 0;
+};
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Launch plan for the weight-streaming kernel. `rows_per_chunk` rows of x go
+// to each blockIdx.y chunk. epi == EPI_ARGMAX forces S == 1.
+Plan make_plan(int ct, int wt, int64_t M, int64_t N, int64_t K, int epi, int rows_per_chunk) {
+  Plan p;
+  p.ct = ct;
+  p.wt = wt;
+  const int cb = dtype_bytes(ct), wb = dtype_bytes(wt);
+  if (!fast_pair(ct, wt) || M <= 0 || N <= 0 || K <= 0) return p;
+  if (K % (16 / cb) != 0 || K % (16 / wb) != 0) return p;
+  if (epi == EPI_ARGMAX && wt != ct) return p;
+  p.rows_per_chunk = rows_per_chunk;
+  p.chunks = (int)((M + rows_per_chunk - 1) / rows_per_chunk);
+  const int rows = (int)(M < rows_per_chunk ? M : rows_per_chunk);
+  p.mt = (rows + 15) / 16;
+  int variant = 0, splits = -1;
+  tune_override(variant, splits);
+  if (variant >= num_variants(ct)) variant = 0;
+  p.variant = variant;
+  p.var = get_variant(ct, wt, variant);
+  const int LG = p.var.wbl / wb;
+  p.KB = 4 * LG;
+  p.NG = p.var.wn * p.var.nsub * 16;
+  p.G = (int)((N + p.NG - 1) / p.NG);
+  p.nkb = (int)((K + p.KB - 1) / p.KB);
+  int S = 1;
+  if (epi == EPI_LINEAR) {
+    const int rounds = (p.nkb + p.var.wk - 1) / p.var.wk;
+    S = splits > 0 ? splits : (kTargetBlocks + p.G * p.chunks / 2) / (p.G * p.chunks);
+    if (S < 1) S = 1;
+    if (S > rounds) S = rounds;
+    // split-K needs one counter per (chunk, group) in the counter prefix
+    if ((int64_t)p.chunks * p.G > kCounterSlots) S = 1;
+  } else if (p.chunks > kCounterSlots) {
+    return Plan{};
+  }
+  // K-blocks per split, rounded to whole rounds of WK blocks; drop empty splits.
+  int rounds_per = ((p.nkb + p.var.wk - 1) / p.var.wk + S - 1) / S;
+  p.kb_per = rounds_per * p.var.wk;
+  p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  const int total = p.G * p.S;
+  p.xcd_map = (total % 8 == 0 && (total / 8) % p.S == 0) ? 1 : 0;
+  const int MPAD = p.mt * 16;
+  const int64_t Npad = (int64_t)p.G * p.NG;
+  // Layout: [counter prefix | partials]. Counters always start at offset 0
+  // and every launch leaves the ones it used at zero, so one workspace can
+  // serve any sequence of calls with different shapes and kernels.
+  size_t off = kCounterBytes;
+  p.ticket_off = 0;
+  if (epi == EPI_LINEAR) {
+    if (p.S > 1) {
+      p.part_off = off;
+      off += align_up((size_t)p.chunks * p.S * MPAD * Npad * 4, 256);
+      p.sqp_off = off;
+      off += align_up((size_t)p.chunks * p.G * p.S * MPAD * 4, 256);
+    } else {
+      off = 0;  // no workspace at all
+    }
+  } else {
+    p.aval_off = off;
+    off += align_up((size_t)p.chunks * p.G * MPAD * 4, 256);
+    p.aidx_off = off;
+    off += align_up((size_t)p.chunks * p.G * MPAD * 4, 256);
+  }
+  p.total = off;
+  p.generic = false;
+  return p;
+}
+
+int launch_ws(const Plan &p, WsArgs &a, int epi, void *ws, hipStream_t st) {
+  WsKernel k = pick_kernel(p.ct, p.wt, p.mt, p.variant, epi);
+  if (!k) return MTP_ERR_DTYPE;
+  unsigned char *w8 = (unsigned char *)ws;
+  a.rows_per_chunk = p.rows_per_chunk;
+  a.S = p.S;
+  a.G = p.G;
+  a.kb_per = p.kb_per;
+  a.nkb = p.nkb;
+  a.xcd_map = p.xcd_map;
+  if (epi == EPI_LINEAR) {
+    if (p.S > 1) {
+      a.part = (float *)(w8 + p.part_off);
+      a.sqp = (float *)(w8 + p.sqp_off);
+      a.ticket = (unsigned *)(w8 + p.ticket_off);
+    }
+  } else {
+    a.amax_val = (float *)(w8 + p.aval_off);
+    a.amax_idx = (int *)(w8 + p.aidx_off);
+    a.ticket = (unsigned *)(w8 + p.ticket_off);
+  }
+  const int threads = p.var.wn * p.var.wk * 64;
+  dim3 grid((unsigned)(p.G * p.S), (unsigned)p.chunks, 1);
+  hipLaunchKernelGGL(k, grid, dim3(threads), 0, st, a);
+  return launch_status();
+}
+
+int launch_generic_linear(const void *x, int xt, const void *w, int wt, const float *wscale,
+                          const void *i4scale, int i4dt, int group, int nib, const void *gamma,
+                          int gt, const void *bias, int bt, void *y, int64_t M, int64_t N,
+                          int64_t K, float eps, float scale, int norm, hipStream_t st) {
+  if (M > 65535) return MTP_ERR_SHAPE;
+  dim3 grid((unsigned)((N + 255) / 256), (unsigned)M, 1);
+  hipLaunchKernelGGL(generic_rmsnorm_linear_kernel, grid, dim3(256), 0, st, x, xt, w, wt,
+                     wscale, i4scale, i4dt, group, nib, gamma, gt, bias, bt, y, xt, (int)M,
+                     (int)N, (int)K, eps, scale, norm);
+  return launch_status();
+}
+
+// Shared body of the three RMSNorm -> linear entry points (float / fp8 weights).
+int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void *w, int wt,
+                        int64_t N, const float *wscale, const void *bias, int bt,
+                        const void *gamma, int gt, float eps, float scale, int norm, void *y,
+                        void *ws, size_t ws_bytes, void *stream) {
+  if (!is_float_dt(xt)) return MTP_ERR_DTYPE;
+  if (!(is_float_dt(wt) || wt == MTP_FP8E4M3)) return MTP_ERR_DTYPE;
+  if (bias && !is_float_dt(bt)) return MTP_ERR_DTYPE;
+  if (gamma && !is_float_dt(gt)) return MTP_ERR_DTYPE;
+  if (M < 0 || N < 0 || K < 0 || N > INT32_MAX || K > INT32_MAX || M > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (M == 0 || N == 0) return MTP_OK;
+  if (!x && K > 0) return MTP_ERR_NULL;
+  if ((!w && K > 0) || !y) return MTP_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  Plan p = make_plan(xt, wt, M, N, K, EPI_LINEAR, 64);
+  const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!gamma || aligned16(gamma));
+  if (p.generic || !aligned) {
+    return launch_generic_linear(x, xt, w, wt, wscale, nullptr, 0, 0, -1, gamma, gt, bias, bt, y,
+                                 M, N, K, eps, scale, norm, st);
+  }
+  if (p.total > 0 && (!ws || ws_bytes < p.total)) return MTP_ERR_WORKSPACE;
+  WsArgs a{};
+  a.x = x;
+  a.w = w;
+  a.wscale = wscale;
+  a.gamma = gamma;
+  a.gamma_dt = gt;
+  a.bias = bias;
+  a.bias_dt = bt;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.eps = eps;
+  a.scale = scale;
+  a.norm = norm;
+  return launch_ws(p, a, EPI_LINEAR, ws, st);
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+int mtp_abi_version(void) { return MTP_ABI_VERSION; }
+
+const char *mtp_status_string(int status) {
+  switch (status) {
+    case MTP_OK: return "ok";
+    case MTP_ERR_NULL: return "required pointer is NULL";
+    case MTP_ERR_SHAPE: return "inconsistent or unsupported sizes";
+    case MTP_ERR_DTYPE: return "unsupported dtype or dtype combination";
+    case MTP_ERR_WORKSPACE: return "workspace missing or too small";
+    case MTP_ERR_ALIGN: return "pointer alignment not supported";
+    case MTP_ERR_LAUNCH: return "HIP launch failed";
+    case MTP_ERR_ARG: return "invalid argument";
+  }
+  return "unknown status";
+}
+
+const char *mtp_last_hip_error(void) { return g_last_hip_error; }
+
+size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, int64_t N,
+                                          int64_t K) {
+  if (w_kind == MTP_U8) return 0;  // packed INT4: no split-K workspace yet
+  Plan p = make_plan(x_dtype, w_kind, M, N, K, EPI_LINEAR, 64);
+  return p.generic ? 0 : p.total;
+}
+
+int mtp_fused_rmsnorm_linear(const void *x, int x_dtype, int64_t M, int64_t K, const void *weight,
+                             int w_dtype, int64_t N, const void *bias, int bias_dtype,
+                             const void *gamma, int gamma_dtype, float eps, float scale, int norm,
+                             void *y, void *workspace, size_t workspace_bytes, void *stream) {
+  if (!is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
+  return rmsnorm_linear_impl(x, x_dtype, M, K, weight, w_dtype, N, nullptr, bias, bias_dtype,
+                             gamma, gamma_dtype, eps, scale, norm, y, workspace, workspace_bytes,
+                             stream);
+}
+
+int mtp_fused_rmsnorm_linear_fp8(const void *x, int x_dtype, int64_t M, int64_t K,
+                                 const void *weight_fp8, int w_dtype, const float *wscale,
+                                 int64_t N, const void *bias, int bias_dtype, const void *gamma,
+                                 int gamma_dtype, float eps, int norm, void *y, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  if (!wscale && N > 0 && M > 0) return MTP_ERR_NULL;
+  return rmsnorm_linear_impl(x, x_dtype, M, K, weight_fp8, w_dtype, N, wscale, bias,
+                             bias_dtype, gamma, gamma_dtype, eps, 1.0f, norm, y, workspace,
+                             workspace_bytes, stream);
+}
+
+int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K, const uint8_t *packed,
+                          const void *scales, int scale_dtype, int64_t N, int64_t group,
+                          int nibble, const void *gamma, int gamma_dtype, float eps, int norm,
+                          void *y, void *workspace, size_t workspace_bytes, void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (!is_float_dt(x_dtype)) return MTP_ERR_DTYPE;
+  if (scale_dtype != MTP_F32 && scale_dtype != MTP_F16 && scale_dtype != MTP_BF16)
+    return MTP_ERR_DTYPE;
+  if (gamma && !is_float_dt(gamma_dtype)) return MTP_ERR_DTYPE;
+  if (nibble != MTP_NIBBLE_OFFSET8 && nibble != MTP_NIBBLE_TWOS) return MTP_ERR_ARG;
+  if (M < 0 || N < 0 || K < 0 || group <= 0 || (K & 1) || (group & 1) || M > INT32_MAX ||
+      N > INT32_MAX || K > INT32_MAX || group > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (M == 0 || N == 0) return MTP_OK;
+  if (!y || (K > 0 && (!x || !packed || !scales))) return MTP_ERR_NULL;
+  return launch_generic_linear(x, x_dtype, packed, MTP_U8, nullptr, scales, scale_dtype,
+                               (int)group, nibble, gamma, gamma_dtype, nullptr, 0, y, M, N, K,
+                               eps, 1.0f, norm, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+static int verify_rows_per_chunk(int64_t seq) { return (int)((64 / seq) * seq); }
+
+size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq, int64_t V, int64_t K) {
+  if (seq < 1 || seq > 64) return 0;
+  Plan p = make_plan(h_dtype, h_dtype, rows, V, K, EPI_ARGMAX, verify_rows_per_chunk(seq));
+  return p.generic ? 0 : p.total;
+}
+
+static int verify_common(const void *hidden, int ht, int64_t rows, int64_t K, const void *w,
+                         int wt, int64_t V, const void *bias, int bt, int rows_per_chunk,
+                         WsArgs &a, void *ws, size_t ws_bytes, void *stream) {
+  Plan p = make_plan(ht, wt, rows, V, K, EPI_ARGMAX, rows_per_chunk);
+  if (p.generic) return MTP_ERR_SHAPE;
+  if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;
+  if (!ws || ws_bytes < p.total) return MTP_ERR_WORKSPACE;
+  a.x = hidden;
+  a.w = w;
+  a.bias = bias;
+  a.bias_dt = bt;
+  a.M = (int)rows;
+  a.N = (int)V;
+  a.K = (int)K;
+  a.scale = 1.0f;
+  return launch_ws(p, a, EPI_ARGMAX, ws, (hipStream_t)stream);
+}
+
+int mtp_fused_verify(const void *hidden, int h_dtype, int64_t M, int64_t K, const void *weight,
+                     int w_dtype, int64_t V, const void *bias, int bias_dtype,
+                     const int32_t *draft, int8_t *accept, int32_t *top, void *workspace,
+                     size_t workspace_bytes, void *stream) {
+  if (!is_float_dt(h_dtype) || w_dtype != h_dtype) return MTP_ERR_DTYPE;
+  if (bias && !is_float_dt(bias_dtype)) return MTP_ERR_DTYPE;
+  if (M < 0 || K <= 0 || V <= 0 || M > INT32_MAX || K > INT32_MAX || V > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (M == 0) return MTP_OK;
+  if (!hidden || !weight || !draft || !accept || !top) return MTP_ERR_NULL;
+  WsArgs a{};
+  a.draft = draft;
+  a.accept = accept;
+  a.top = top;
+  a.multi = 0;
+  return verify_common(hidden, h_dtype, M, K, weight, w_dtype, V, bias, bias_dtype, 64, a,
+                       workspace, workspace_bytes, stream);
+}
+
+int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B, int64_t S, int64_t K,
+                           const void *weight, int w_dtype, int64_t V, const void *bias,
+                           int bias_dtype, const int32_t *draft, int64_t D, int8_t *accept,
+                           int32_t *accepted_n, int32_t *corrected, int32_t *top_out,
+                           void *workspace, size_t workspace_bytes, void *stream) {
+  if (!is_float_dt(h_dtype) || w_dtype != h_dtype) return MTP_ERR_DTYPE;
+  if (bias && !is_float_dt(bias_dtype)) return MTP_ERR_DTYPE;
+  if (B < 0 || S < 1 || D < 0 || S != D + 1 || K <= 0 || V <= 0 || S > 64 ||
+      B * S > INT32_MAX || K > INT32_MAX || V > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (B == 0) return MTP_OK;
+  if (!hidden || !weight || !accepted_n || !corrected || (D > 0 && (!draft || !accept)))
+    return MTP_ERR_NULL;
+  WsArgs a{};
+  a.draft = draft;
+  a.accept = accept;
+  a.accepted_n = accepted_n;
+  a.corrected = corrected;
+  a.top = top_out;
+  a.multi = 1;
+  a.S_seq = (int)S;
+  a.D = (int)D;
+  const int rpc = verify_rows_per_chunk(S);
+  return verify_common(hidden, h_dtype, B * S, K, weight, w_dtype, V, bias, bias_dtype, rpc, a,
+                       workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,586 @@
+// Skinny-M weight-streaming GEMM for gfx950: the engine of the RMSNorm ->
+// linear family and of the verify lm_head pass.
+//
+// Problem: y[M, N] = epilogue( x[M, K] . W[N, K]^T ) with at most 64 rows of
+// x per row chunk (tree-node counts / verify rows) and large N, K. W
+// dominates the traffic and is read exactly once; the work is HBM-bound.
+//
+// Work decomposition
+//   workgroup  = WN x WK waves; it owns NG = WN * NW output columns
+//                (NW = 16 * NSUB per wave) and a contiguous K-range (split
+//                `sp` of S cross-workgroup K-splits).
+//   wave (wn, wk) streams W rows [n0 + wn*NW, +NW) over the K-blocks
+//                kb = kbA + r*WK + wk of its workgroup's range, straight from
+//                HBM into VGPRs with 16-byte non-temporal loads and one
+//                K-block of look-ahead (double-buffered registers).
+//   x            the waves of wk-group wk stage the x K-block their group
+//                consumes into LDS: fp32 upcast, sum of squares for the
+//                RMSNorm statistic, optional gamma multiply, rounding to the
+//                MFMA input type, written in MFMA-fragment order so every
+//                B-operand read is one conflict-free ds_read_b128.
+//                Double-buffered across rounds, one barrier per round.
+//   MFMA         D[n][m] += W[n, k] x[m, k]: A = W (16 rows of n), B = x
+//                (16 columns of m), 16x16x32 bf16/f16 or 16x16x4 f32.
+//                Inside a K-block, lane group g covers the contiguous
+//                k-range [g*LG, (g+1)*LG), so each lane's W bytes are one
+//                contiguous run (4 lanes read 4*WBL contiguous bytes of a W
+//                row); x is staged with the same permutation of k.
+//   reduction    waves wk > 0 hand their accumulators to wk == 0 through
+//                LDS (fixed order); then either the epilogue runs directly
+//                (S == 1), or fp32 partials go to the workspace and the last
+//                workgroup of the column group (atomic ticket between
+//                agent-scope fences) sums the S partials in split order and
+//                runs it, then re-arms the ticket for the next launch.
+// Row statistics are applied in the epilogue: rstd[m] * (x[m] . W[n]) equals
+// (x[m] * rstd[m]) . W[n] up to fp32 rounding, so MFMA inputs stay exact.
+#pragma once
+
+#include "mtp_common.hpp"
+
+namespace mtp {
+
+enum { EPI_LINEAR = 0, EPI_ARGMAX = 1 };
+
+struct WsArgs {
+  // operands
+  const void *x;        // [M, K] CT
+  const void *w;        // [N, K] WT
+  const float *wscale;  // [N] or null (per output channel)
+  const void *gamma;    // [K] gamma_dt or null
+  const void *bias;     // [N] bias_dt or null
+  void *y;              // [M, N] CT (EPI_LINEAR)
+  int gamma_dt, bias_dt;
+  int M, N, K;
+  float eps, scale;
+  int norm;
+  // decomposition
+  int rows_per_chunk;  // rows of x per blockIdx.y chunk (<= MT * 16)
+  int S;               // K-splits
+  int G;               // column groups = ceil(N / NG)
+  int kb_per;          // K-blocks per split
+  int nkb;             // total K-blocks = ceil(K / KB)
+  int xcd_map;         // 1: blockIdx -> (group, split) keeps a group's splits on one XCD
+  // workspace (per row chunk; the kernel adds the chunk offset)
+  float *part;       // [chunks][S][MPAD][G*NG]          split-K partials
+  float *sqp;        // [chunks][G][S][MPAD]             partial sums of squares
+  unsigned *ticket;  // [chunks][G] (EPI_LINEAR) / [chunks] (EPI_ARGMAX)
+  float *amax_val;   // [chunks][G][MPAD]                (EPI_ARGMAX)
+  int *amax_idx;     // [chunks][G][MPAD]                (EPI_ARGMAX)
+  // verify (EPI_ARGMAX)
+  const int32_t *draft;  // [B, D] (multi) or [M] (single)
+  int8_t *accept;
+  int32_t *accepted_n;
+  int32_t *corrected;
+  int32_t *top;  // [rows] or null
+  int S_seq, D;  // multi-verify: hidden rows per batch element, drafts
+  int multi;     // 1: chain acceptance, 0: single-token verify
+};
+
+template <int CT, int WT, int WBL>
+struct WsShape {
+  static constexpr int kCtBytes = dtype_bytes(CT);
+  static constexpr int kWBytes = dtype_bytes(WT);
+  static constexpr int LG = WBL / kWBytes;  // k per lane group per K-block
+  static constexpr int KB = 4 * LG;         // k per K-block
+  static constexpr int NWL = WBL / 16;      // 16-byte W loads per lane per subtile
+  static constexpr int E = 16 / kCtBytes;   // x elements per 16-byte chunk
+  static constexpr int CPR = KB / E;        // x chunks per row per K-block
+  static constexpr int CPG = LG / E;        // x chunks per lane group
+  static constexpr int STEPS = (CT == MTP_F32) ? LG : LG / 8;
+};
+
+// Load E gamma values for k .. k+E-1 (16-byte aligned chunk) as fp32.
+template <int E>
+__device__ __forceinline__ void load_gamma_chunk(const void *g, int dt, int k, float (&out)[E]) {
+  if (dt == MTP_F32) {
+    const u32x4 *p = (const u32x4 *)((const float *)g + k);
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q) {
+      const u32x4 v = p[q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[4 * q + e] = __uint_as_float(v[e]);
+    }
+  } else {
+    const uint16_t *p16 = (const uint16_t *)g + k;
+    uint32_t d[E / 2];
+    if constexpr (E == 8) {
+      const u32x4 v = *(const u32x4 *)p16;
+      d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+    } else {
+      const uint2 v = *(const uint2 *)p16;
+      d[0] = v.x; d[1] = v.y;
+    }
+#pragma unroll
+    for (int q = 0; q < E / 2; ++q) {
+      f32x2 t = dt == MTP_BF16 ? unpack2<MTP_BF16>(d[q]) : unpack2<MTP_F16>(d[q]);
+      out[2 * q] = t[0];
+      out[2 * q + 1] = t[1];
+    }
+  }
+}
+
+template <int CT, int WT, int MT, int NSUB, int WN, int WK, int WBL, int EPI>
+__global__ void __launch_bounds__(WN * WK * 64)
+wstream_kernel(const WsArgs a) {
+  using Sh = WsShape<CT, WT, WBL>;
+  constexpr int NT = WN * WK * 64;
+  constexpr int TW = WN * 64;  // staging threads per wk-group
+  constexpr int MPAD = MT * 16;
+  constexpr int NW = NSUB * 16;
+  constexpr int NG = WN * NW;
+  constexpr int LG = Sh::LG, KB = Sh::KB, NWL = Sh::NWL, E = Sh::E;
+  constexpr int CPR = Sh::CPR, CPG = Sh::CPG;
+  constexpr int BLK_SLOTS = MT * CPG * 64;  // 16-byte LDS slots per K-block
+  constexpr int ROUND_SLOTS = WK * BLK_SLOTS;
+  constexpr int PPB = MPAD * CPR;            // x chunks per K-block
+  constexpr int XIT = (PPB + TW - 1) / TW;   // chunks per staging thread
+  constexpr int QR = TW / CPR;               // rows covered per staging iteration
+  static_assert(CPR <= 64 && 64 % CPR == 0, "row chunks must tile a wave");
+
+  constexpr int XBUF_BYTES = 2 * ROUND_SLOTS * 16;
+  constexpr int RED_BYTES = (WK > 1) ? (WK - 1) * WN * 64 * MT * NSUB * 16 : 16;
+  constexpr int POOL_BYTES = XBUF_BYTES > RED_BYTES ? XBUF_BYTES : RED_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char pool[POOL_BYTES];
+  __shared__ float sq_red[WK * XIT * QR];
+  __shared__ float sq_row[MPAD];
+  __shared__ int s_flag;
+  __shared__ float s_bval[WN][MPAD];
+  __shared__ int s_bidx[WN][MPAD];
+  __shared__ int s_top[MPAD];
+
+  u32x4 *xbuf = (u32x4 *)pool;
+
+  const int th = threadIdx.x;
+  const int lane = th & 63;
+  const int wave = th >> 6;
+  const int wn = wave % WN;
+  const int wk = wave / WN;
+  const int lg = lane >> 4;
+  const int l16 = lane & 15;
+
+  // ---- block -> (column group, split), XCD-aware -------------------------
+  int bid = blockIdx.x;
+  if (a.xcd_map) {
+    const int per = (a.G * a.S) >> 3;  // host guarantees divisibility
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  const int grp = bid / a.S;
+  const int sp = bid - grp * a.S;
+  const int mchunk = blockIdx.y;
+  const int m0 = mchunk * a.rows_per_chunk;
+  const int Mloc = min(a.rows_per_chunk, a.M - m0);
+  const int K = a.K, N = a.N;
+
+  const int kbA = sp * a.kb_per;
+  const int kbB = min(a.nkb, kbA + a.kb_per);
+  const int nrounds = (kbB - kbA + WK - 1) / WK;
+  const int n_wave0 = grp * NG + wn * NW;
+
+  // ---- W streaming --------------------------------------------------------
+  const int64_t ldw = (int64_t)K * Sh::kWBytes;
+  const unsigned char *wrow[NSUB];
+#pragma unroll
+  for (int u = 0; u < NSUB; ++u) {
+    int n = n_wave0 + u * 16 + l16;
+    n = n < N ? n : N - 1;  // rows past N are computed and discarded
+    wrow[u] = (const unsigned char *)a.w + (int64_t)n * ldw + (int64_t)lg * LG * Sh::kWBytes;
+  }
+
+  auto load_w = [&](u32x4 (&wr)[NSUB][NWL], int kb) {
+    const int kq = kb * KB + lg * LG;
+#pragma unroll
+    for (int j = 0; j < NWL; ++j) {
+      const bool ok = (kb < kbB) && (kq + j * (16 / Sh::kWBytes) < K);
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u)
+        wr[u][j] = ok ? ld_nt16(wrow[u] + (int64_t)kb * KB * Sh::kWBytes + j * 16)
+                      : u32x4{0, 0, 0, 0};
+    }
+  };
+
+  // ---- x staging: thread -> (wk-group, chunk column), rows q0 + i*QR ------
+  const unsigned char *xbase = (const unsigned char *)a.x + (int64_t)m0 * K * Sh::kCtBytes;
+  const int s_wk = th / TW;
+  const int tw = th % TW;
+  const int my_c = tw % CPR;
+  const int q0 = tw / CPR;
+  const int my_k_off = my_c * E;
+  const int my_g = my_k_off / LG;
+  const int my_j = (my_k_off % LG) / E;
+  u32x4 xr[XIT];
+  float gv[E];
+  float sq[XIT];
+#pragma unroll
+  for (int i = 0; i < XIT; ++i) sq[i] = 0.f;
+
+  auto load_x = [&](int r) {
+    const int kb = kbA + r * WK + s_wk;
+    const int k = kb * KB + my_k_off;
+    const bool kok = kb < kbB && k < K;
+#pragma unroll
+    for (int i = 0; i < XIT; ++i) {
+      const int m = q0 + i * QR;
+      xr[i] = (kok && m < Mloc && m < MPAD) ? ld16(xbase + ((int64_t)m * K + k) * Sh::kCtBytes)
+                                            : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) gv[e] = 1.f;
+    if (a.gamma && kok) load_gamma_chunk<E>(a.gamma, a.gamma_dt, k, gv);
+  };
+
+  auto store_x = [&](int buf) {
+    u32x4 *dst = xbuf + buf * ROUND_SLOTS + s_wk * BLK_SLOTS;
+#pragma unroll
+    for (int i = 0; i < XIT; ++i) {
+      const int m = q0 + i * QR;
+      if (m >= MPAD) continue;
+      float v[E];
+      if constexpr (CT == MTP_F32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(xr[i][e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f32x2 t = unpack2<CT>(xr[i][e]);
+          v[2 * e] = t[0];
+          v[2 * e + 1] = t[1];
+        }
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) s += v[e] * v[e];
+      sq[i] += s;
+      u32x4 o;
+      if constexpr (CT == MTP_F32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = __float_as_uint(v[e] * gv[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack2<CT>(v[2 * e] * gv[2 * e], v[2 * e + 1] * gv[2 * e + 1]);
+      }
+      dst[((m >> 4) * CPG + my_j) * 64 + (m & 15) + 16 * my_g] = o;
+    }
+  };
+
+  // ---- MFMA over one K-block ----------------------------------------------
+  f32x4 acc[MT][NSUB];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const u32x4 (&wr)[NSUB][NWL], int buf) {
+    const u32x4 *src = xbuf + buf * ROUND_SLOTS + wk * BLK_SLOTS;
+    if constexpr (CT == MTP_F32) {
+      // 16x16x4 f32: one k per lane per step; x slot j holds steps 4j .. 4j+3.
+#pragma unroll
+      for (int j = 0; j < CPG; ++j) {
+        u32x4 xb[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) xb[t] = src[(t * CPG + j) * 64 + lane];
+        float wv[NSUB][4];
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+          if constexpr (WT == MTP_F32) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wv[u][e] = __uint_as_float(wr[u][j][e]);
+          } else {  // fp8: the 4 values of dword (j & 3) of load (j >> 2)
+            const uint32_t d = wr[u][j >> 2][j & 3];
+            const f32x2 lo = fp8x2_to_f32(d, false), hi = fp8x2_to_f32(d, true);
+            wv[u][0] = lo[0]; wv[u][1] = lo[1]; wv[u][2] = hi[0]; wv[u][3] = hi[1];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const float bv = __uint_as_float(xb[t][e]);
+#pragma unroll
+            for (int u = 0; u < NSUB; ++u) acc[t][u] = mfma16_f32(wv[u][e], bv, acc[t][u]);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < Sh::STEPS; ++s) {
+        u32x4 av[NSUB];
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+          if constexpr (WT == CT) {
+            av[u] = wr[u][s];
+          } else {  // fp8 -> CT, 8 values per step
+            const u32x4 q = wr[u][s >> 1];
+            const uint32_t d0 = (s & 1) ? q[2] : q[0];
+            const uint32_t d1 = (s & 1) ? q[3] : q[1];
+            av[u][0] = fp8x2_to_ct<CT, false>(d0);
+            av[u][1] = fp8x2_to_ct<CT, true>(d0);
+            av[u][2] = fp8x2_to_ct<CT, false>(d1);
+            av[u][3] = fp8x2_to_ct<CT, true>(d1);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const u32x4 bv = src[(t * CPG + s) * 64 + lane];
+#pragma unroll
+          for (int u = 0; u < NSUB; ++u) acc[t][u] = mfma16<CT>(av[u], bv, acc[t][u]);
+        }
+      }
+    }
+  };
+
+  // ---- main loop --------------------------------------------------------------
+  u32x4 wA[NSUB][NWL], wB[NSUB][NWL];
+  if (nrounds > 0) {
+    load_w(wA, kbA + wk);
+    load_x(0);
+    store_x(0);
+  }
+  __syncthreads();
+  for (int r = 0; r < nrounds; r += 2) {
+    const bool more1 = r + 1 < nrounds;
+    if (more1) {
+      load_w(wB, kbA + (r + 1) * WK + wk);
+      load_x(r + 1);
+    }
+    compute(wA, 0);
+    if (more1) store_x(1);
+    __syncthreads();
+    if (!more1) break;
+    const bool more2 = r + 2 < nrounds;
+    if (more2) {
+      load_w(wA, kbA + (r + 2) * WK + wk);
+      load_x(r + 2);
+    }
+    compute(wB, 1);
+    if (more2) store_x(0);
+    __syncthreads();
+  }
+
+  // ---- row statistics over this K-range -----------------------------------------
+#pragma unroll
+  for (int i = 0; i < XIT; ++i) {
+    float s = sq[i];
+#pragma unroll
+    for (int off = 1; off < CPR; off <<= 1) s += __shfl_xor(s, off, 64);
+    if (my_c == 0) sq_red[(s_wk * XIT + i) * QR + q0] = s;
+  }
+  __syncthreads();
+  if (th < MPAD) {
+    float s = 0.f;
+    for (int q = 0; q < WK; ++q) s += sq_red[(q * XIT + th / QR) * QR + th % QR];
+    sq_row[th] = s;
+  }
+
+  // ---- cross-wave K reduction (fixed order) -------------------------------------
+  if constexpr (WK > 1) {
+    f32x4 *red = (f32x4 *)pool;  // x buffers are dead: all waves passed the last barrier
+    if (wk > 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+          red[(((wk - 1) * WN + wn) * (MT * NSUB) + t * NSUB + u) * 64 + lane] = acc[t][u];
+    }
+    __syncthreads();
+    if (wk == 0) {
+      for (int q = 1; q < WK; ++q)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int u = 0; u < NSUB; ++u)
+            acc[t][u] += red[(((q - 1) * WN + wn) * (MT * NSUB) + t * NSUB + u) * 64 + lane];
+    }
+  }
+  __syncthreads();
+
+  const int Npad = a.G * NG;
+
+  if constexpr (EPI == EPI_LINEAR) {
+    // v = columns n .. n+3 of local row m; sqsum = the row's sum of squares.
+    auto finish = [&](int m, int n, f32x4 v, float sqsum) {
+      const float rs = a.norm ? 1.0f / sqrtf(sqsum / (float)K + a.eps) : 1.0f;
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nn = min(n + j, N - 1);
+        float t = v[j] * rs;
+        if (a.wscale) t *= a.wscale[nn];
+        if (a.bias) t += load_as_f32(a.bias, a.bias_dt, nn);
+        o[j] = t * a.scale;
+      }
+      const int64_t base = (int64_t)(m0 + m) * N + n;
+      if (n + 3 < N && (N & 3) == 0) {
+        if constexpr (CT == MTP_F32) {
+          *(f32x4 *)((float *)a.y + base) = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+          uint2 pk;
+          pk.x = pack2<CT>(o[0], o[1]);
+          pk.y = pack2<CT>(o[2], o[3]);
+          *(uint2 *)((uint16_t *)a.y + base) = pk;
+        }
+      } else {
+        for (int j = 0; j < 4; ++j)
+          if (n + j < N) store_from_f32(a.y, CT, base + j, o[j]);
+      }
+    };
+
+    if (a.S == 1) {
+      if (wk == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int m = t * 16 + l16;
+          if (m >= Mloc) continue;
+          const float sqs = sq_row[m];
+#pragma unroll
+          for (int u = 0; u < NSUB; ++u) {
+            const int n = n_wave0 + u * 16 + 4 * lg;
+            if (n < N) finish(m, n, acc[t][u], sqs);
+          }
+        }
+      }
+      return;
+    }
+
+    // split-K: publish partials; the last workgroup of the group reduces.
+    float *part = a.part + (int64_t)mchunk * a.S * MPAD * Npad;
+    float *sqp = a.sqp + (int64_t)mchunk * a.G * a.S * MPAD;
+    unsigned *ticket = a.ticket + (int64_t)mchunk * a.G;
+    if (wk == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int m = t * 16 + l16;
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+          const int n = n_wave0 + u * 16 + 4 * lg;
+          *(f32x4 *)(part + ((int64_t)sp * MPAD + m) * Npad + n) = acc[t][u];
+        }
+      }
+    }
+    if (th < MPAD) sqp[((int64_t)grp * a.S + sp) * MPAD + th] = sq_row[th];
+    __threadfence();
+    __syncthreads();
+    if (th == 0) s_flag = (atomicAdd(ticket + grp, 1u) == (unsigned)(a.S - 1));
+    __syncthreads();
+    if (!s_flag) return;
+    __threadfence();
+    constexpr int Q = NG / 4;
+    for (int item = th; item < MPAD * Q; item += NT) {
+      const int m = item / Q;
+      const int n = grp * NG + 4 * (item - m * Q);
+      if (m >= Mloc || n >= N) continue;
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      float ss = 0.f;
+      for (int q = 0; q < a.S; ++q) {
+        s += *(const f32x4 *)(part + ((int64_t)q * MPAD + m) * Npad + n);
+        ss += sqp[((int64_t)grp * a.S + q) * MPAD + m];
+      }
+      finish(m, n, s, ss);
+    }
+    if (th == 0) ticket[grp] = 0u;
+  } else {
+    // ---- EPI_ARGMAX (S == 1): per-row (max, lowest index) over the group ----
+    if (wk == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int n = n_wave0 + u * 16 + 4 * lg + j;
+            if (n < N) {
+              float v = acc[t][u][j];
+              if (a.bias) v += load_as_f32(a.bias, a.bias_dt, n);
+              if (argmax_better(v, n, bv, bi)) {
+                bv = v;
+                bi = n;
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int off = 16; off < 64; off <<= 1) {
+          const float ov = __shfl_xor(bv, off, 64);
+          const int oi = __shfl_xor(bi, off, 64);
+          if (argmax_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (lg == 0) {
+          s_bval[wn][t * 16 + l16] = bv;
+          s_bidx[wn][t * 16 + l16] = bi;
+        }
+      }
+    }
+    __syncthreads();
+    float *pv = a.amax_val + (int64_t)mchunk * a.G * MPAD;
+    int *pi = a.amax_idx + (int64_t)mchunk * a.G * MPAD;
+    if (th < MPAD) {
+      float bv = s_bval[0][th];
+      int bi = s_bidx[0][th];
+      for (int q = 1; q < WN; ++q)
+        if (argmax_better(s_bval[q][th], s_bidx[q][th], bv, bi)) {
+          bv = s_bval[q][th];
+          bi = s_bidx[q][th];
+        }
+      pv[(int64_t)grp * MPAD + th] = bv;
+      pi[(int64_t)grp * MPAD + th] = bi;
+    }
+    __threadfence();
+    __syncthreads();
+    unsigned *ticket = a.ticket + mchunk;
+    if (th == 0) s_flag = (atomicAdd(ticket, 1u) == (unsigned)(a.G - 1));
+    __syncthreads();
+    if (!s_flag) return;
+    __threadfence();
+    // Final argmax over all groups: wave w handles rows w, w + waves, ...
+    for (int m = wave; m < Mloc; m += WN * WK) {
+      float bv = -__builtin_inff();
+      int bi = 0x7fffffff;
+      for (int gq = lane; gq < a.G; gq += 64) {
+        const float v = pv[(int64_t)gq * MPAD + m];
+        const int ix = pi[(int64_t)gq * MPAD + m];
+        if (argmax_better(v, ix, bv, bi)) {
+          bv = v;
+          bi = ix;
+        }
+      }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (argmax_better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) s_top[m] = bi;
+    }
+    __syncthreads();
+    if (a.top)
+      for (int m = th; m < Mloc; m += NT) a.top[m0 + m] = s_top[m];
+    if (!a.multi) {
+      for (int m = th; m < Mloc; m += NT) a.accept[m0 + m] = (int8_t)(s_top[m] == a.draft[m0 + m]);
+    } else {
+      const int Sq = a.S_seq, Dd = a.D;
+      const int b0 = m0 / Sq;
+      for (int bl = th; bl < Mloc / Sq; bl += NT) {
+        const int b = b0 + bl;
+        const int *tp = s_top + bl * Sq;
+        a.corrected[b] = tp[0];
+        int n = 0;
+        for (int d = 0; d < Dd; ++d) {
+          const bool ok = (tp[d + 1] == a.draft[(int64_t)b * Dd + d]) && (n == d);
+          a.accept[(int64_t)b * Dd + d] = (int8_t)ok;
+          if (ok) n = d + 1;
+        }
+        a.accepted_n[b] = n;
+      }
+    }
+    if (th == 0) *ticket = 0u;
+  }
+}
+
+}  // namespace mtp

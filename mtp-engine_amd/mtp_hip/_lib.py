@@ -1,0 +1,130 @@
+"""ctypes binding of libmtp_hip.so (the C ABI in include/mtp_hip.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already loaded (both carry the soname libamdhip64.so.7); the kernels then run
+on torch's streams and memory. A missing library is an error, never a silent
+fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime first)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmtp_hip.so")
+
+# dtype codes (enum mtp_dtype)
+F32, BF16, F16, FP8E4M3, U8, I8, I32, I64 = range(8)
+# status codes (enum mtp_status)
+OK = 0
+ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_WORKSPACE, ERR_ALIGN, ERR_LAUNCH, ERR_ARG = range(-1, -8, -1)
+NIBBLE_OFFSET8, NIBBLE_TWOS = 0, 1
+
+_TORCH_CODES = {
+    torch.float32: F32,
+    torch.bfloat16: BF16,
+    torch.float16: F16,
+    torch.float8_e4m3fn: FP8E4M3,
+    torch.uint8: U8,
+    torch.int8: I8,
+    torch.int32: I32,
+    torch.int64: I64,
+}
+
+# Every symbol include/mtp_hip.h declares, with its ctypes signature.
+_vp, _i, _i64, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+SIGNATURES = {
+    "mtp_abi_version": (_i, []),
+    "mtp_status_string": (ctypes.c_char_p, [_i]),
+    "mtp_last_hip_error": (ctypes.c_char_p, []),
+    "mtp_fused_rmsnorm_linear": (
+        _i, [_vp, _i, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i, _f, _f, _i, _vp, _vp, _sz, _vp]),
+    "mtp_fused_rmsnorm_linear_fp8": (
+        _i, [_vp, _i, _i64, _i64, _vp, _i, _vp, _i64, _vp, _i, _vp, _i, _f, _i, _vp, _vp, _sz, _vp]),
+    "mtp_fused_int4_matmul": (
+        _i, [_vp, _i, _i64, _i64, _vp, _vp, _i, _i64, _i64, _i, _vp, _i, _f, _i, _vp, _vp, _sz, _vp]),
+    "mtp_rmsnorm_linear_workspace_bytes": (_sz, [_i, _i, _i64, _i64, _i64]),
+    "mtp_fused_verify": (
+        _i, [_vp, _i, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_fused_multi_verify": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i64, _vp, _vp, _vp, _vp,
+             _vp, _sz, _vp]),
+    "mtp_verify_workspace_bytes": (_sz, [_i, _i64, _i64, _i64, _i64]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class MtpHipError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise MtpHipError(
+                    f"{LIB_PATH} is missing: build it with `python mtp-engine_amd/build.py`")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def code(dtype: torch.dtype) -> int:
+    try:
+        return _TORCH_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}") from None
+
+
+def check(status: int, what: str) -> None:
+    """Map a status code to the exception the reference's wrappers raise."""
+    if status == OK:
+        return
+    lib = load()
+    msg = lib.mtp_status_string(status).decode()
+    if status == ERR_LAUNCH:
+        msg += ": " + lib.mtp_last_hip_error().decode()
+    if status == ERR_SHAPE:
+        raise AssertionError(f"{what}: {msg}")
+    if status == ERR_DTYPE:
+        raise TypeError(f"{what}: {msg}")
+    raise MtpHipError(f"{what}: {msg} (status {status})")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# ---------------------------------------------------------------------------
+# Workspace: one zero-initialised buffer per (device, stream), grown on
+# demand. Kernels leave their counters at zero, so the buffer is reused as is.
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 0 if ws is None else 2 * ws.numel())
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws

@@ -1,0 +1,125 @@
+"""Drop-in for the reference module ``mtp_kernels`` (RMSNorm -> linear family)
+on MI355X.
+
+Same names, argument order, defaults and return values as the reference's
+wrappers (mtp_kernels.py:936-977, 1014-1044, 1194-1219, 1336-1353); every
+entry point launches a hand-written gfx950 kernel through libmtp_hip.so.
+Keyword-only extensions: ``gamma`` (RMSNorm weight, default None = the
+reference) and ``norm`` (False = plain linear, the mode CachedLinear needs)
+on the RMSNorm -> linear entry points; ``nibble``, ``gamma``, ``norm`` and
+``eps`` on fused_int4_matmul (default = the reference: offset-8 nibbles, no
+norm).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import torch
+
+from mtp_hip import ops
+
+
+@dataclass(frozen=True)
+class KernelTuningConfig:
+    """Launch defaults of the reference (mtp_kernels.py:54-65). Only
+    ``fp8_scale`` (the default ``scale`` of fused_rmsnorm_linear) is read;
+    tile shapes come from the library's own tables."""
+    BLOCK_M: int = 64
+    BLOCK_N: int = 64
+    BLOCK_K: int = 32
+    BLOCK_DHEAD: int = 64
+    num_warps: int = 4
+    num_stages: int = 2
+    fp8_scale: float = 1.0
+
+
+TUNING = KernelTuningConfig()
+MAX_FP8 = 448.0
+
+
+def fused_rmsnorm_linear(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+    scale: Optional[float] = None,
+    *,
+    gamma: Optional[torch.Tensor] = None,
+    norm: bool = True,
+) -> torch.Tensor:
+    """((x * rsqrt(mean(x^2) + eps) [* gamma]) @ weight.T + bias) * scale in
+    x.dtype (mtp_kernels.py:936-977). The bias is cast to x.dtype first, as
+    the reference does (line 952)."""
+    if scale is None:
+        scale = TUNING.fp8_scale
+    if bias is not None:
+        bias = bias.to(dtype=x.dtype, device=x.device)
+    return ops.rmsnorm_linear(x, weight, bias, eps, scale, gamma=gamma, norm=norm)
+
+
+def fused_rmsnorm_linear_fp8(
+    x: torch.Tensor,
+    weight_fp8: torch.Tensor,
+    wscale: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+    *,
+    gamma: Optional[torch.Tensor] = None,
+    norm: bool = True,
+) -> torch.Tensor:
+    """(x * rstd [* gamma]) @ (float(W) * wscale[:, None]).T + bias in
+    x.dtype (mtp_kernels.py:1014-1044)."""
+    return ops.rmsnorm_linear_fp8(x, weight_fp8, wscale, bias, eps, gamma=gamma, norm=norm)
+
+
+def fused_int4_matmul(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    K: int,
+    group: int = 32,
+    *,
+    nibble: str = "ref",
+    gamma: Optional[torch.Tensor] = None,
+    norm: bool = False,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """x @ dequantize_int4(packed, scales, K, group).T in x.dtype
+    (mtp_kernels.py:1194-1219). nibble="ref" decodes nibble n as n - 8 (the
+    reference decoder); "twos" reads two's-complement nibbles."""
+    return ops.int4_matmul(x, packed, scales, K, group, nibble=nibble, gamma=gamma, norm=norm,
+                           eps=eps)
+
+
+def pack_scales(weight_scales: List[torch.Tensor],
+                kv_scales: Optional[List[torch.Tensor]] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One flat fp32 buffer holding every scale tensor back to back, plus the
+    int64 offsets [0, n0, n0+n1, ...] (mtp_kernels.py:1336-1346)."""
+    all_scales = list(weight_scales) + list(kv_scales or [])
+    sizes = [int(s.numel()) for s in all_scales]
+    offs = [0]
+    for n in sizes:
+        offs.append(offs[-1] + n)
+    flat = torch.cat([s.reshape(-1).to(torch.float32) for s in all_scales])
+    return flat, torch.tensor(offs, dtype=torch.int64, device=flat.device)
+
+
+def unpack_scale_tensor(flat: torch.Tensor, offsets: torch.Tensor, idx: int,
+                        shape: Tuple[int, ...]) -> torch.Tensor:
+    """View of scale tensor ``idx`` inside the packed buffer
+    (mtp_kernels.py:1349-1353)."""
+    start, end = int(offsets[idx]), int(offsets[idx + 1])
+    return flat[start:end].view(*shape)
+
+
+__all__ = [
+    "KernelTuningConfig",
+    "TUNING",
+    "MAX_FP8",
+    "fused_rmsnorm_linear",
+    "fused_rmsnorm_linear_fp8",
+    "fused_int4_matmul",
+    "pack_scales",
+    "unpack_scale_tensor",
+]

@@ -1,0 +1,187 @@
+"""GPU parity of the RMSNorm -> linear family (fp32 / bf16 / f16 / fp8
+weights) against the CPU oracle on identical seeded inputs.
+
+Tolerance: |y - ref| <= rtol * (|ref| + RMS(ref)) with rtol 1e-5 for fp32
+(TF32 off) and 2e-2 for bf16 / f16 / fp8 outputs."""
+import os
+
+import pytest
+import torch
+
+from conftest import close
+from oracle import eager as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _tune_reset():
+    old = os.environ.pop("MTP_WS_TUNE", None)
+    yield
+    os.environ.pop("MTP_WS_TUNE", None)
+    if old is not None:
+        os.environ["MTP_WS_TUNE"] = old
+
+
+def _inputs(M, N, K, dtype, seed, bias=True, gamma=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    W = (0.05 * torch.randn(N, K, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(N, generator=g)).to(dtype) if bias else None
+    gm = (1 + 0.1 * torch.randn(K, generator=g)) if gamma else None
+    return x, W, b, gm
+
+
+def _dev(t):
+    return None if t is None else t.to(DEV)
+
+
+SHAPES = [(16, 4096, 1024), (1, 64, 64), (5, 128, 64), (17, 100, 256), (33, 1000, 136),
+          (64, 512, 1024), (70, 256, 512), (130, 96, 64)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_rmsnorm_linear_matches_oracle(dtype, M, N, K):
+    from mtp_hip import ops
+    x, W, b, gm = _inputs(M, N, K, dtype, seed=M * 7 + N + K)
+    print(f"case dtype={dtype} M={M} N={N} K={K}", flush=True)
+    y = ops.rmsnorm_linear(_dev(x), _dev(W), _dev(b), 1e-6, 0.75, gamma=_dev(gm))
+    torch.cuda.synchronize()
+    ref = O.rmsnorm_linear(x, W, b, 1e-6, 0.75, gamma=gm)
+    assert y.dtype == dtype and y.shape == (M, N)
+    ok, worst = close(y, ref, RTOL[dtype])
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("tune", ["0,1", "0,3", "1,1", "1,4", "2,2", "3,5", "3,1"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_tile_variants_and_splits(tune, dtype):
+    from mtp_hip import ops
+    os.environ["MTP_WS_TUNE"] = tune
+    M, N, K = 40, 1040, 1536
+    x, W, b, gm = _inputs(M, N, K, dtype, seed=11)
+    print(f"case tune={tune} dtype={dtype}", flush=True)
+    y = ops.rmsnorm_linear(_dev(x), _dev(W), _dev(b), 1e-6, 1.0, gamma=_dev(gm))
+    torch.cuda.synchronize()
+    ref = O.rmsnorm_linear(x, W, b, 1e-6, 1.0, gamma=gm)
+    ok, worst = close(y, ref, RTOL[dtype])
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
+def test_no_norm_no_gamma_no_bias_and_generic_path():
+    from mtp_hip import ops
+    # K = 100 is not a multiple of the 16-byte vector: the generic kernel runs.
+    for (M, N, K) in [(7, 48, 64), (7, 48, 100)]:
+        x, W, _, _ = _inputs(M, N, K, torch.bfloat16, seed=3, bias=False, gamma=False)
+        y = ops.rmsnorm_linear(_dev(x), _dev(W), None, 1e-6, 1.0, norm=False)
+        ref = O.rmsnorm_linear(x, W, None, 1e-6, 1.0, norm=False)
+        ok, worst = close(y, ref, 2e-2)
+        assert ok, (M, N, K, worst)
+
+
+def test_reference_self_checks():
+    """The reference's own checks on its seeded inputs: fused linear max abs
+    error < 1e-4 (test_engine.py:5, mtp_engine.py:1644-1651) and the fp8
+    entry with fp32 weights in +-448 (mtp_engine.py:1792-1800)."""
+    import mtp_kernels as MK
+    torch.manual_seed(1)
+    x = torch.randn(5, 64)
+    W = torch.randn(128, 64)
+    b = torch.randn(128)
+    y = MK.fused_rmsnorm_linear(x.to(DEV), W.to(DEV), b.to(DEV), 1e-6).cpu()
+    xn = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6)
+    assert (y - torch.nn.functional.linear(xn, W, b)).abs().max().item() < 1e-4
+    Wsw = torch.randn(32, 64)
+    row_scale = Wsw.abs().max(dim=-1, keepdim=True).values.squeeze(-1) / 448.0
+    Wf8 = (Wsw / row_scale[:, None]).clamp(-448, 448)
+    xq = torch.randn(4, 64)
+    y8 = MK.fused_rmsnorm_linear_fp8(xq.to(DEV), Wf8.to(DEV), row_scale.to(DEV)).cpu()
+    xn = xq * torch.rsqrt((xq * xq).mean(-1, keepdim=True) + 1e-6)
+    y8_ref = torch.nn.functional.linear(xn, Wf8.float() * row_scale[:, None])
+    assert (y8 - y8_ref).abs().max().item() < 1e-4
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 48, 64), (20, 272, 528), (64, 1024, 2048), (9, 40, 80)])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fp8_weights_match_oracle(M, N, K, xdtype):
+    from mtp_hip import ops
+    g = torch.Generator().manual_seed(M + N)
+    W = 0.02 * torch.randn(N, K, generator=g)
+    wq, ws = O.quantize_fp8_per_channel(W)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = 0.1 * torch.randn(N, generator=g)
+    print(f"case fp8 M={M} N={N} K={K} x={xdtype}", flush=True)
+    y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
+    ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+    ok, worst = close(y, ref, RTOL[xdtype])
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("M", [8, 32, 64])
+def test_fp8_workload_full_size(M):
+    """The fp8-e4m3 RMSNorm+linear workload: x bf16 [M,4096], W [14336,4096]."""
+    from mtp_hip import ops, workloads
+    d = workloads.fp8_linear(M)
+    print(f"case fp8 workload M={M}", flush=True)
+    y = ops.rmsnorm_linear_fp8(_dev(d["x"]), _dev(d["weight_fp8"]), _dev(d["wscale"]), None,
+                               d["eps"], gamma=_dev(d["gamma"]))
+    ref = O.rmsnorm_linear_fp8(d["x"], d["weight_fp8"], d["wscale"], None, d["eps"],
+                               gamma=d["gamma"])
+    ok, worst = close(y, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+    # size-independent property: deterministic (fixed split order) bit for bit
+    y2 = ops.rmsnorm_linear_fp8(_dev(d["x"]), _dev(d["weight_fp8"]), _dev(d["wscale"]), None,
+                                d["eps"], gamma=_dev(d["gamma"]))
+    assert torch.equal(y, y2)
+
+
+def test_fp32_workload_full_size():
+    """fp32 RMSNorm+linear workload (x[16,1024], W[4096,1024]), rtol 1e-5."""
+    from mtp_hip import ops, workloads
+    d = workloads.fp32_linear()
+    y = ops.rmsnorm_linear(_dev(d["x"]), _dev(d["weight"]), None, d["eps"], 1.0,
+                           gamma=_dev(d["gamma"]))
+    ref = O.rmsnorm_linear(d["x"], d["weight"], None, d["eps"], 1.0, gamma=d["gamma"])
+    ok, worst = close(y, ref, 1e-5)
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
+def test_graph_replay_matches_eager():
+    """Captured into a HIP graph, every replay equals the eager result (the
+    kernel re-arms its split-K tickets itself)."""
+    from mtp_hip import ops
+    M, N, K = 32, 2048, 2048
+    x, W, b, gm = _inputs(M, N, K, torch.bfloat16, seed=5)
+    x, W, b, gm = _dev(x), _dev(W), _dev(b), _dev(gm)
+    eager = ops.rmsnorm_linear(x, W, b, 1e-6, 1.0, gamma=gm)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            ops.rmsnorm_linear(x, W, b, 1e-6, 1.0, gamma=gm)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.rmsnorm_linear(x, W, b, 1e-6, 1.0, gamma=gm)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        _ = (x.float() * 2).sum()  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_cached_linear_drop_in():
+    from mtp_perf_hardening import CachedLinear
+    torch.manual_seed(0)
+    lin = CachedLinear(64, 96).to(DEV)
+    x = torch.randn(2, 3, 64, device=DEV)
+    y = lin(x)
+    ref = torch.nn.functional.linear(x.cpu(), lin.weight.detach().cpu(), lin.bias.detach().cpu())
+    ok, worst = close(y.reshape(-1, 96), ref.reshape(-1, 96), 1e-5)
+    assert ok and y.shape == (2, 3, 96), worst

@@ -1,0 +1,174 @@
+"""GPU parity of fused_verify / fused_multi_verify against the CPU oracle.
+
+Token ids, accepted lengths, rollback indices and corrected tokens must be
+bit-exact wherever the oracle's top-2 logit gap exceeds TAU (logits that
+close can legitimately swap under a different fp32 summation order); rows
+whose first low-gap position is at or before the first rejection are
+excluded from the chain checks and counted."""
+import pytest
+import torch
+
+from oracle import eager as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check_tokens(top_gpu, top_ref, gap, tau):
+    top_gpu = top_gpu.cpu().reshape(-1)
+    top_ref = top_ref.reshape(-1)
+    sure = (gap.reshape(-1) > tau)
+    assert sure.float().mean() > 0.9, "too many near-ties for a meaningful check"
+    assert torch.equal(top_gpu[sure], top_ref[sure].to(top_gpu.dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K,V", [(4, 64, 256), (1, 128, 1000), (70, 256, 3000), (9, 512, 50257)])
+def test_fused_verify_matches_oracle(dtype, M, K, V):
+    import mtp_fused_verify as FV
+    g = torch.Generator().manual_seed(M + K + V)
+    h = torch.randn(M, K, generator=g).to(dtype)
+    W = (0.05 * torch.randn(V, K, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(V, generator=g)).to(dtype)
+    _, top_ref = O.fused_verify(h, W, torch.zeros(M), b)
+    top_ref_i, gap = O.logits_top(h, W, b)
+    draft = top_ref.clone().to(torch.int64)
+    draft[::2] = (draft[::2] + 1) % V  # half the rows rejected
+    print(f"case verify dtype={dtype} M={M} K={K} V={V}", flush=True)
+    acc, top = FV.fused_verify(h.to(DEV), W.to(DEV), draft.to(DEV), b.to(DEV))
+    torch.cuda.synchronize()
+    assert acc.dtype == torch.int8 and top.dtype == torch.int32
+    _check_tokens(top, top_ref_i, gap, 1e-3)
+    sure = gap > 1e-3
+    exp_acc = (top_ref == draft.to(torch.int32)).to(torch.int8)
+    assert torch.equal(acc.cpu()[sure], exp_acc[sure])
+
+
+def test_verify_planted_ties_and_nan():
+    from mtp_hip import ops
+    V, K = 700, 64
+    W = torch.zeros(V, K)
+    W[10, :] = 1.0
+    W[650, :] = 1.0  # tie with row 10 across column groups: 10 must win
+    h = torch.ones(3, K)
+    h[2] = -1.0
+    acc, top = ops.verify(h.to(DEV), W.to(DEV), torch.tensor([10, 0, 0]).to(DEV))
+    assert top.cpu().tolist()[:2] == [10, 10]
+    assert int(top.cpu()[2]) == 0  # all others 0, rows 10/650 at -K: the first zero wins
+    assert acc.cpu().tolist() == [1, 0, 1]
+    Wn = W.clone()
+    Wn[333, 0] = float("nan")
+    _, topn = ops.verify(h.to(DEV), Wn.to(DEV), torch.zeros(3, dtype=torch.int64).to(DEV))
+    assert topn.cpu().tolist() == [333, 333, 333]  # NaN is the maximum
+
+
+def test_reference_multi_verify_check_seeded():
+    """test_new_features.py:34-56 on the same seeded inputs."""
+    import mtp_fused_verify as FV
+    torch.manual_seed(1)
+    B, S, K, V, D = 2, 5, 64, 256, 4
+    hidden = torch.randn(B, S, K)
+    W = torch.randn(V, K)
+    b = torch.randn(V)
+    draft = torch.randint(0, V, (B, D))
+    accept, accepted_n, corrected = FV.fused_multi_verify(hidden.to(DEV), W.to(DEV),
+                                                          draft.to(DEV), b.to(DEV))
+    top = torch.nn.functional.linear(hidden, W, b).argmax(-1)
+    for i in range(B):
+        ref_n = 0
+        for d in range(D):
+            if top[i, d + 1] == draft[i, d]:
+                ref_n = d + 1
+            else:
+                break
+        assert accepted_n[i].item() == ref_n
+        assert corrected[i].item() == top[i, 0].item()
+        # prefix-masked: ones on the accepted prefix, zeros from the first rejection on
+        assert accept[i].tolist() == [1] * ref_n + [0] * (D - ref_n)
+
+
+def _chain_case(B, D, K, V, dtype, seed, bias):
+    from mtp_hip import workloads
+    g = torch.Generator().manual_seed(seed)
+    hidden = torch.randn(B, D + 1, K, generator=g).to(dtype)
+    W = (0.05 * torch.randn(V, K, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(V, generator=g)).to(dtype) if bias else None
+    top, gap = O.logits_top(hidden.reshape(-1, K), W, b)
+    draft = workloads.make_chain_drafts(top.reshape(B, D + 1), V, seed)
+    return hidden, W, b, draft, top.reshape(B, D + 1), gap.reshape(B, D + 1)
+
+
+def _check_chain(out, hidden, W, b, draft, tau):
+    accept, accepted_n, corrected, top = [t.cpu() for t in out]
+    ra, rn, rc, rtop, gap = O.fused_multi_verify(hidden, W, draft, b)
+    B, S = rtop.shape
+    excluded = 0
+    for i in range(B):
+        first_bad = next((s for s in range(S) if not gap[i, s] > tau), S)
+        if first_bad <= int(rn[i]) + 1:  # a near-tie at or before the first rejection
+            excluded += 1
+            continue
+        assert int(accepted_n[i]) == int(rn[i]), i
+        assert int(corrected[i]) == int(rc[i]), i
+        assert torch.equal(accept[i], ra[i]), i
+    assert excluded <= B // 4 + 1, f"excluded {excluded} of {B}"
+    sure = gap > tau
+    assert torch.equal(top[sure], rtop[sure])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,D,K,V,bias", [(2, 4, 64, 256, True), (20, 4, 128, 5000, False),
+                                          (3, 0, 64, 300, True), (7, 8, 256, 20000, True)])
+def test_multi_verify_matches_oracle(dtype, B, D, K, V, bias):
+    from mtp_hip import ops
+    hidden, W, b, draft, _, _ = _chain_case(B, D, K, V, dtype, seed=B * 31 + V, bias=bias)
+    print(f"case multi dtype={dtype} B={B} D={D} K={K} V={V}", flush=True)
+    out = ops.multi_verify(hidden.to(DEV), W.to(DEV), draft.to(DEV),
+                           None if b is None else b.to(DEV), return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hidden, W, b, draft, 1e-3)
+
+
+def test_workspace_shared_across_kernels_and_shapes():
+    """Split-K linear, verify and multi-verify calls of different shapes share
+    one per-stream workspace; each must still match the oracle (the arrival
+    counters live in a fixed prefix that every launch leaves at zero)."""
+    from mtp_hip import ops
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn(48, 1024, generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(3000, 1024, generator=g)).to(torch.bfloat16)
+    h = torch.randn(3, 5, 256, generator=g).to(torch.bfloat16)
+    Wv = (0.05 * torch.randn(6000, 256, generator=g)).to(torch.bfloat16)
+    ref_y = O.rmsnorm_linear(x, W, None, 1e-6)
+    top, gap = O.logits_top(h.reshape(-1, 256), Wv)
+    draft = top.reshape(3, 5)[:, 1:].to(torch.int64)
+    for rep in range(3):
+        y = ops.rmsnorm_linear(x.to(DEV), W.to(DEV), None, 1e-6)
+        _, _, _, t = ops.multi_verify(h.to(DEV), Wv.to(DEV), draft.to(DEV), return_top=True)
+        _, t1 = ops.verify(h.reshape(-1, 256).to(DEV), Wv.to(DEV), top.to(DEV))
+        torch.cuda.synchronize()
+        from conftest import close
+        assert close(y, ref_y, 2e-2)[0], rep
+        sure = gap > 1e-3
+        assert torch.equal(t.cpu().reshape(-1)[sure], top[sure]), rep
+        assert torch.equal(t1.cpu()[sure], top[sure]), rep
+
+
+def test_multi_verify_workload_full_size():
+    """The multi-verify workload: 8 x (4+1) hidden bf16 [40,4096], lm_head
+    [128256,4096] bf16, geometric(0.6) accepted prefixes."""
+    from mtp_hip import ops, workloads
+    d = workloads.multi_verify()
+    hidden, W = d["hidden"], d["weight"]
+    top, gap = O.logits_top(hidden.reshape(-1, hidden.shape[-1]), W)
+    draft = workloads.make_chain_drafts(top.reshape(d["B"], d["D"] + 1), W.shape[0], d["seed"])
+    print("case multi-verify workload", flush=True)
+    Wd = W.to(DEV)
+    out = ops.multi_verify(hidden.to(DEV), Wd, draft.to(DEV), None, return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hidden, W, None, draft, 1e-4)
+    # rollback consumer on device outputs equals the oracle's
+    ra, rn, rc, _, _ = O.fused_multi_verify(hidden, W, draft)
+    got = O.engine_rollback(out[0], out[1], out[2], draft)
+    exp = O.engine_rollback(ra, rn, rc, draft)
+    assert got[:2] == exp[:2] and torch.equal(got[2], exp[2])
