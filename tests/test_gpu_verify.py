@@ -105,7 +105,7 @@ def _check_chain(out, hidden, W, b, draft, tau):
     excluded = 0
     for i in range(B):
         first_bad = next((s for s in range(S) if not gap[i, s] > tau), S)
-        if first_bad <= int(rn[i]) + 1:  # a near-tie at or before the first rejection
+        if first_bad < S and first_bad <= int(rn[i]) + 1:  # near-tie at/before the first rejection
             excluded += 1
             continue
         assert int(accepted_n[i]) == int(rn[i]), i
