@@ -148,4 +148,35 @@ __device__ __forceinline__ u32x4 ld_nt16(const void *p) {
 }
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
 
+// ---- cross-workgroup hand-off without an L2 write-back ---------------------
+// An agent-scope release fence writes back the whole L2 of the XCD
+// (buffer_wbl2), which serialises badly when every workgroup of a launch
+// does it. Data handed between workgroups is therefore only ever accessed
+// through agent-scope atomics (global_load/store ... sc1: coherent across
+// XCDs): the producer publishes with atomic stores, waits until they have
+// completed (s_waitcnt), then bumps the arrival ticket with a relaxed atomic
+// RMW (performed at the device coherence point); the consumer that sees the
+// final count reads the data back with agent-scope atomic loads.
+__device__ __forceinline__ void pub_f32(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub_i32(int *p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_f32(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int get_i32(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every thread: wait for its own stores/atomics to complete.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+// Relaxed arrival count (returns the previous value).
+__device__ __forceinline__ unsigned ticket_add(unsigned *t) {
+  return __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ticket_reset(unsigned *t) {
+  __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace mtp

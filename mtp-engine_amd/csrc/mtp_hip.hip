@@ -73,6 +73,10 @@ Plan make_plan(int ct, int wt, int64_t M, int64_t N, int64_t K, int epi, int row
   if (!fast_pair(ct, wt) || M <= 0 || N <= 0 || K <= 0) return p;
   if (K % (16 / cb) != 0 || K % (16 / wb) != 0) return p;
   if (epi == EPI_ARGMAX && wt != ct) return p;
+  // buffer descriptors span one column group of W and one row chunk of x;
+  // both must stay below the out-of-range offset 2^31
+  if ((int64_t)256 * K * wb >= (int64_t)1 << 31 || (int64_t)64 * K * cb >= (int64_t)1 << 31)
+    return p;
   p.rows_per_chunk = rows_per_chunk;
   p.chunks = (int)((M + rows_per_chunk - 1) / rows_per_chunk);
   const int rows = (int)(M < rows_per_chunk ? M : rows_per_chunk);
@@ -158,6 +162,108 @@ int launch_ws(const Plan &p, WsArgs &a, int epi, void *ws, hipStream_t st) {
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// x-resident linear kernel: plan and launch.
+constexpr size_t kLdsXBudget = 144 * 1024;  // resident x per workgroup
+constexpr size_t kLdsMax = 150 * 1024;      // dynamic LDS limit we allow
+constexpr int kWsxMinBlocks = 200;           // aim for most of the 256 CUs busy
+
+struct PlanX {
+  bool ok = false;
+  int ct = 0, wt = 0, mt = 0, variant = 0;
+  Variant var{};
+  int NG = 0, KB = 0, G = 0, S = 1, kb_per = 0, nkb = 0;
+  int rows_per_chunk = 64, chunks = 0, xcd_map = 0;
+  size_t lds = 0, part_off = 0, sqp_off = 0, total = 0;
+};
+
+PlanX make_plan_x(int ct, int wt, int64_t M, int64_t N, int64_t K) {
+  PlanX p;
+  p.ct = ct;
+  p.wt = wt;
+  const int cb = dtype_bytes(ct), wb = dtype_bytes(wt);
+  if (!fast_pair(ct, wt) || M <= 0 || N <= 0 || K <= 0) return p;
+  if (K % (16 / cb) != 0 || K % (16 / wb) != 0) return p;
+  if ((int64_t)256 * K * wb >= (int64_t)1 << 31 || (int64_t)64 * K * cb >= (int64_t)1 << 31)
+    return p;
+  p.chunks = (int)((M + 63) / 64);
+  const int rows = (int)(M < 64 ? M : 64);
+  p.mt = (rows + 15) / 16;
+  int variant = rows <= 16 ? 0 : 1, splits = -1;
+  tune_override(variant, splits);
+  if (variant >= kWsxNumVar) variant = 0;
+  p.variant = variant;
+  p.var = wsx_variant(ct, wt, variant);
+  const int LG = p.var.wbl / wb;
+  p.KB = 4 * LG;
+  p.NG = p.var.wn * p.var.nsub * 16;
+  p.G = (int)((N + p.NG - 1) / p.NG);
+  p.nkb = (int)((K + p.KB - 1) / p.KB);
+  const int MPAD = p.mt * 16;
+  const size_t blk = (size_t)MPAD * p.KB * cb;
+  const int kb_max = (int)(kLdsXBudget / blk);
+  if (kb_max < 1) return p;
+  int S = (p.nkb + kb_max - 1) / kb_max;
+  if (splits > 0) {
+    S = splits > S ? splits : S;
+  } else {
+    // more K-splits while the grid is short of CUs and every wave keeps >= 2 K-blocks
+    while ((int64_t)p.G * S * p.chunks < kWsxMinBlocks && p.nkb / (S + 1) >= 2 * p.var.wk) ++S;
+  }
+  if (S > p.nkb) S = p.nkb;
+  if (S > 1 && (int64_t)p.chunks * p.G > kCounterSlots) return p;
+  p.kb_per = (p.nkb + S - 1) / S;
+  p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  const int total = p.G * p.S;
+  p.xcd_map = (total % 8 == 0 && (total / 8) % p.S == 0) ? 1 : 0;
+  // the all-wave reduction parks every wave's accumulators in the x region
+  const size_t red = (size_t)p.var.wk * p.var.wn * 64 * p.mt * p.var.nsub * 16;
+  p.lds = (size_t)p.kb_per * blk;
+  if (red > p.lds) p.lds = red;
+  if (p.lds > kLdsMax) return p;
+  const int64_t Npad = (int64_t)p.G * p.NG;
+  // split-K partials of one row chunk sit behind one buffer descriptor
+  if (p.S > 1 && (int64_t)p.S * MPAD * Npad * 4 >= (int64_t)1 << 31) return p;
+  size_t off = 0;
+  if (p.S > 1) {
+    off = kCounterBytes;
+    p.part_off = off;
+    off += align_up((size_t)p.chunks * p.S * MPAD * Npad * 4, 256);
+    p.sqp_off = off;
+    off += align_up((size_t)p.chunks * p.G * p.S * MPAD * 4, 256);
+  }
+  p.total = off;
+  p.ok = true;
+  return p;
+}
+
+int launch_wsx(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
+  WsKernel k = wsx_pick_kernel(p.ct, p.wt, p.mt, p.variant);
+  if (!k) return MTP_ERR_DTYPE;
+  unsigned char *w8 = (unsigned char *)ws;
+  a.rows_per_chunk = 64;
+  a.S = p.S;
+  a.G = p.G;
+  a.kb_per = p.kb_per;
+  a.nkb = p.nkb;
+  a.xcd_map = p.xcd_map;
+  if (p.S > 1) {
+    a.part = (float *)(w8 + p.part_off);
+    a.sqp = (float *)(w8 + p.sqp_off);
+    a.ticket = (unsigned *)w8;
+  }
+  const hipError_t e = hipFuncSetAttribute((const void *)k,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
+  if (e != hipSuccess) {
+    std::strncpy(g_last_hip_error, hipGetErrorString(e), sizeof(g_last_hip_error) - 1);
+    return MTP_ERR_LAUNCH;
+  }
+  const int threads = p.var.wn * p.var.wk * 64;
+  dim3 grid((unsigned)(p.G * p.S), (unsigned)p.chunks, 1);
+  hipLaunchKernelGGL(k, grid, dim3(threads), p.lds, st, a);
+  return launch_status();
+}
+
 int launch_generic_linear(const void *x, int xt, const void *w, int wt, const float *wscale,
                           const void *i4scale, int i4dt, int group, int nib, const void *gamma,
                           int gt, const void *bias, int bt, void *y, int64_t M, int64_t N,
@@ -185,9 +291,10 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   if (!x && K > 0) return MTP_ERR_NULL;
   if ((!w && K > 0) || !y) return MTP_ERR_NULL;
   hipStream_t st = (hipStream_t)stream;
-  Plan p = make_plan(xt, wt, M, N, K, EPI_LINEAR, 64);
+  PlanX p = make_plan_x(xt, wt, M, N, K);
   const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!gamma || aligned16(gamma));
-  if (p.generic || !aligned) {
+  // the tiled kernel reads gamma as fp32 (the Python shim upcasts it)
+  if (!p.ok || !aligned || (gamma && gt != MTP_F32)) {
     return launch_generic_linear(x, xt, w, wt, wscale, nullptr, 0, 0, -1, gamma, gt, bias, bt, y,
                                  M, N, K, eps, scale, norm, st);
   }
@@ -196,8 +303,7 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.x = x;
   a.w = w;
   a.wscale = wscale;
-  a.gamma = gamma;
-  a.gamma_dt = gt;
+  a.gamma = (const float *)gamma;
   a.bias = bias;
   a.bias_dt = bt;
   a.y = y;
@@ -207,7 +313,7 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
-  return launch_ws(p, a, EPI_LINEAR, ws, st);
+  return launch_wsx(p, a, ws, st);
 }
 
 }  // namespace
@@ -236,8 +342,8 @@ const char *mtp_last_hip_error(void) { return g_last_hip_error; }
 size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, int64_t N,
                                           int64_t K) {
   if (w_kind == MTP_U8) return 0;  // packed INT4: no split-K workspace yet
-  Plan p = make_plan(x_dtype, w_kind, M, N, K, EPI_LINEAR, 64);
-  return p.generic ? 0 : p.total;
+  PlanX p = make_plan_x(x_dtype, w_kind, M, N, K);
+  return p.ok ? p.total : 0;
 }
 
 int mtp_fused_rmsnorm_linear(const void *x, int x_dtype, int64_t M, int64_t K, const void *weight,

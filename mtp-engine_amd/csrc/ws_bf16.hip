@@ -14,3 +14,13 @@ WsKernel ws_pick_bf16(int wt, int mt, int v, int epi) {
 }
 
 }  // namespace mtp
+
+namespace mtp {
+
+WsKernel wsx_pick_bf16(int wt, int mt, int v) {
+  if (wt == MTP_BF16) return wsx_pick<MTP_BF16, MTP_BF16>(mt, v);
+  if (wt == MTP_FP8E4M3) return wsx_pick<MTP_BF16, MTP_FP8E4M3>(mt, v);
+  return nullptr;
+}
+
+}  // namespace mtp

@@ -14,3 +14,13 @@ WsKernel ws_pick_f32(int wt, int mt, int v, int epi) {
 }
 
 }  // namespace mtp
+
+namespace mtp {
+
+WsKernel wsx_pick_f32(int wt, int mt, int v) {
+  if (wt == MTP_F32) return wsx_pick<MTP_F32, MTP_F32>(mt, v);
+  if (wt == MTP_FP8E4M3) return wsx_pick<MTP_F32, MTP_FP8E4M3>(mt, v);
+  return nullptr;
+}
+
+}  // namespace mtp

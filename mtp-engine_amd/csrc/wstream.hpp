@@ -11,26 +11,32 @@
 //                `sp` of S cross-workgroup K-splits).
 //   wave (wn, wk) streams W rows [n0 + wn*NW, +NW) over the K-blocks
 //                kb = kbA + r*WK + wk of its workgroup's range, straight from
-//                HBM into VGPRs with 16-byte non-temporal loads and one
-//                K-block of look-ahead (double-buffered registers).
+//                HBM into VGPRs with 16-byte buffer loads and one K-block of
+//                look-ahead (double-buffered registers). Buffer descriptors
+//                bound every stream, so rows past N or M read as zero with no
+//                branch; K-tail chunks get an out-of-range offset.
 //   x            the waves of wk-group wk stage the x K-block their group
 //                consumes into LDS: fp32 upcast, sum of squares for the
 //                RMSNorm statistic, optional gamma multiply, rounding to the
 //                MFMA input type, written in MFMA-fragment order so every
 //                B-operand read is one conflict-free ds_read_b128.
-//                Double-buffered across rounds, one barrier per round.
+//                Double-buffered across rounds, one barrier per round; the
+//                next round's x loads are issued before its W loads, so the
+//                wait for x leaves the W prefetch in flight (vmcnt retires in
+//                issue order).
 //   MFMA         D[n][m] += W[n, k] x[m, k]: A = W (16 rows of n), B = x
 //                (16 columns of m), 16x16x32 bf16/f16 or 16x16x4 f32.
-//                Inside a K-block, lane group g covers the contiguous
-//                k-range [g*LG, (g+1)*LG), so each lane's W bytes are one
-//                contiguous run (4 lanes read 4*WBL contiguous bytes of a W
-//                row); x is staged with the same permutation of k.
+//                Inside a K-block, load j of lane group g reads 16-byte chunk
+//                4j + g of the row's K-block segment, so the four lanes of a
+//                row read 64 contiguous bytes per instruction; x is staged
+//                with the same permutation of k.
 //   reduction    waves wk > 0 hand their accumulators to wk == 0 through
 //                LDS (fixed order); then either the epilogue runs directly
-//                (S == 1), or fp32 partials go to the workspace and the last
-//                workgroup of the column group (atomic ticket between
-//                agent-scope fences) sums the S partials in split order and
-//                runs it, then re-arms the ticket for the next launch.
+//                (S == 1), or fp32 partials are published to the workspace and
+//                the last workgroup of the column group (relaxed arrival
+//                ticket, agent-scope atomic data accesses: see mtp_common.hpp)
+//                sums the S partials in split order, runs the epilogue and
+//                re-arms the ticket for the next launch.
 // Row statistics are applied in the epilogue: rstd[m] * (x[m] . W[n]) equals
 // (x[m] * rstd[m]) . W[n] up to fp32 rounding, so MFMA inputs stay exact.
 #pragma once
@@ -46,10 +52,10 @@ struct WsArgs {
   const void *x;        // [M, K] CT
   const void *w;        // [N, K] WT
   const float *wscale;  // [N] or null (per output channel)
-  const void *gamma;    // [K] gamma_dt or null
+  const float *gamma;   // [K] fp32 or null
   const void *bias;     // [N] bias_dt or null
   void *y;              // [M, N] CT (EPI_LINEAR)
-  int gamma_dt, bias_dt;
+  int bias_dt;
   int M, N, K;
   float eps, scale;
   int norm;
@@ -89,35 +95,19 @@ struct WsShape {
   static constexpr int STEPS = (CT == MTP_F32) ? LG : LG / 8;
 };
 
-// Load E gamma values for k .. k+E-1 (16-byte aligned chunk) as fp32.
-template <int E>
-__device__ __forceinline__ void load_gamma_chunk(const void *g, int dt, int k, float (&out)[E]) {
-  if (dt == MTP_F32) {
-    const u32x4 *p = (const u32x4 *)((const float *)g + k);
-#pragma unroll
-    for (int q = 0; q < E / 4; ++q) {
-      const u32x4 v = p[q];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) out[4 * q + e] = __uint_as_float(v[e]);
-    }
-  } else {
-    const uint16_t *p16 = (const uint16_t *)g + k;
-    uint32_t d[E / 2];
-    if constexpr (E == 8) {
-      const u32x4 v = *(const u32x4 *)p16;
-      d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
-    } else {
-      const uint2 v = *(const uint2 *)p16;
-      d[0] = v.x; d[1] = v.y;
-    }
-#pragma unroll
-    for (int q = 0; q < E / 2; ++q) {
-      f32x2 t = dt == MTP_BF16 ? unpack2<MTP_BF16>(d[q]) : unpack2<MTP_F16>(d[q]);
-      out[2 * q] = t[0];
-      out[2 * q + 1] = t[1];
-    }
-  }
+// Buffer descriptor over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
 }
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset past any descriptor's range
+// Cache-policy operand of the buffer intrinsics selecting sc1: the same
+// agent-coherent access the compiler emits for agent-scope atomic loads and
+// stores, here 16 bytes wide (see the hand-off notes in mtp_common.hpp).
+constexpr int kSc1 = 16;
 
 template <int CT, int WT, int MT, int NSUB, int WN, int WK, int WBL, int EPI>
 __global__ void __launch_bounds__(WN * WK * 64)
@@ -128,13 +118,14 @@ wstream_kernel(const WsArgs a) {
   constexpr int MPAD = MT * 16;
   constexpr int NW = NSUB * 16;
   constexpr int NG = WN * NW;
-  constexpr int LG = Sh::LG, KB = Sh::KB, NWL = Sh::NWL, E = Sh::E;
+  constexpr int KB = Sh::KB, NWL = Sh::NWL, E = Sh::E;
   constexpr int CPR = Sh::CPR, CPG = Sh::CPG;
   constexpr int BLK_SLOTS = MT * CPG * 64;  // 16-byte LDS slots per K-block
   constexpr int ROUND_SLOTS = WK * BLK_SLOTS;
   constexpr int PPB = MPAD * CPR;            // x chunks per K-block
   constexpr int XIT = (PPB + TW - 1) / TW;   // chunks per staging thread
   constexpr int QR = TW / CPR;               // rows covered per staging iteration
+  constexpr int WE = 16 / Sh::kWBytes;       // W elements per 16-byte chunk
   static_assert(CPR <= 64 && 64 % CPR == 0, "row chunks must tile a wave");
 
   constexpr int XBUF_BYTES = 2 * ROUND_SLOTS * 16;
@@ -176,39 +167,41 @@ wstream_kernel(const WsArgs a) {
   const int nrounds = (kbB - kbA + WK - 1) / WK;
   const int n_wave0 = grp * NG + wn * NW;
 
-  // ---- W streaming --------------------------------------------------------
-  const int64_t ldw = (int64_t)K * Sh::kWBytes;
-  const unsigned char *wrow[NSUB];
+  // ---- W streaming: one descriptor over this group's rows ------------------
+  const uint32_t ldw = (uint32_t)K * Sh::kWBytes;
+  const int grp_rows = min(NG, N - grp * NG);
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc((const unsigned char *)a.w + (int64_t)grp * NG * ldw, (uint32_t)grp_rows * ldw);
+  uint32_t wrow[NSUB];
 #pragma unroll
-  for (int u = 0; u < NSUB; ++u) {
-    int n = n_wave0 + u * 16 + l16;
-    n = n < N ? n : N - 1;  // rows past N are computed and discarded
-    wrow[u] = (const unsigned char *)a.w + (int64_t)n * ldw + (int64_t)lg * LG * Sh::kWBytes;
-  }
+  for (int u = 0; u < NSUB; ++u) wrow[u] = (uint32_t)(wn * NW + u * 16 + l16) * ldw + lg * 16;
 
   auto load_w = [&](u32x4 (&wr)[NSUB][NWL], int kb) {
-    const int kq = kb * KB + lg * LG;
 #pragma unroll
     for (int j = 0; j < NWL; ++j) {
-      const bool ok = (kb < kbB) && (kq + j * (16 / Sh::kWBytes) < K);
+      const bool ok = (kb < kbB) && (kb * KB + (4 * j + lg) * WE < K);
+      const uint32_t koff = (uint32_t)kb * KB * Sh::kWBytes + j * 64;
 #pragma unroll
-      for (int u = 0; u < NSUB; ++u)
-        wr[u][j] = ok ? ld_nt16(wrow[u] + (int64_t)kb * KB * Sh::kWBytes + j * 16)
-                      : u32x4{0, 0, 0, 0};
+      for (int u = 0; u < NSUB; ++u) wr[u][j] = bload16(wrs, ok ? wrow[u] + koff : kOOB);
     }
   };
 
   // ---- x staging: thread -> (wk-group, chunk column), rows q0 + i*QR ------
-  const unsigned char *xbase = (const unsigned char *)a.x + (int64_t)m0 * K * Sh::kCtBytes;
+  const uint32_t ldx = (uint32_t)K * Sh::kCtBytes;
+  const __amdgpu_buffer_rsrc_t xrs =
+      make_rsrc((const unsigned char *)a.x + (int64_t)m0 * ldx, (uint32_t)Mloc * ldx);
+  const __amdgpu_buffer_rsrc_t grs = make_rsrc(a.gamma, a.gamma ? (uint32_t)K * 4u : 0u);
   const int s_wk = th / TW;
   const int tw = th % TW;
   const int my_c = tw % CPR;
   const int q0 = tw / CPR;
   const int my_k_off = my_c * E;
-  const int my_g = my_k_off / LG;
-  const int my_j = (my_k_off % LG) / E;
+  // the W chunk holding this x chunk, its lane group and the MFMA slot
+  const int my_wc = my_k_off / WE;
+  const int my_g = my_wc & 3;
+  const int my_j = (my_wc >> 2) * (WE / E) + (my_k_off % WE) / E;
   u32x4 xr[XIT];
-  float gv[E];
+  u32x4 gr[E / 4];
   float sq[XIT];
 #pragma unroll
   for (int i = 0; i < XIT; ++i) sq[i] = 0.f;
@@ -220,16 +213,18 @@ wstream_kernel(const WsArgs a) {
 #pragma unroll
     for (int i = 0; i < XIT; ++i) {
       const int m = q0 + i * QR;
-      xr[i] = (kok && m < Mloc && m < MPAD) ? ld16(xbase + ((int64_t)m * K + k) * Sh::kCtBytes)
-                                            : u32x4{0, 0, 0, 0};
+      xr[i] = bload16(xrs, (kok && m < MPAD) ? (uint32_t)m * ldx + (uint32_t)k * Sh::kCtBytes : kOOB);
     }
+    // without gamma the descriptor is empty and these loads return zeros
 #pragma unroll
-    for (int e = 0; e < E; ++e) gv[e] = 1.f;
-    if (a.gamma && kok) load_gamma_chunk<E>(a.gamma, a.gamma_dt, k, gv);
+    for (int q = 0; q < E / 4; ++q) gr[q] = bload16(grs, kok ? (uint32_t)(k + 4 * q) * 4u : kOOB);
   };
 
   auto store_x = [&](int buf) {
     u32x4 *dst = xbuf + buf * ROUND_SLOTS + s_wk * BLK_SLOTS;
+    float gv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) gv[e] = a.gamma ? __uint_as_float(gr[e >> 2][e & 3]) : 1.f;
 #pragma unroll
     for (int i = 0; i < XIT; ++i) {
       const int m = q0 + i * QR;
@@ -328,35 +323,43 @@ wstream_kernel(const WsArgs a) {
     }
   };
 
-  // ---- main loop --------------------------------------------------------------
+  // ---- main loop ------------------------------------------------------------
+  // Rounds alternate between register buffers wA / wB and LDS buffers 0 / 1.
+  // Prefetches are issued unconditionally: past the last round they use
+  // out-of-range offsets and return zeros without touching memory, and the
+  // straight-line issue lets the compiler count outstanding loads exactly.
   u32x4 wA[NSUB][NWL], wB[NSUB][NWL];
   if (nrounds > 0) {
-    load_w(wA, kbA + wk);
     load_x(0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wA, kbA + wk);
+    __builtin_amdgcn_sched_barrier(0);
     store_x(0);
   }
   __syncthreads();
-  for (int r = 0; r < nrounds; r += 2) {
-    const bool more1 = r + 1 < nrounds;
-    if (more1) {
-      load_w(wB, kbA + (r + 1) * WK + wk);
-      load_x(r + 1);
-    }
+  int r = 0;
+  for (; r + 1 < nrounds; r += 2) {
+    load_x(r + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wB, kbA + (r + 1) * WK + wk);
+    __builtin_amdgcn_sched_barrier(0);
     compute(wA, 0);
-    if (more1) store_x(1);
+    store_x(1);
     __syncthreads();
-    if (!more1) break;
-    const bool more2 = r + 2 < nrounds;
-    if (more2) {
-      load_w(wA, kbA + (r + 2) * WK + wk);
-      load_x(r + 2);
-    }
+    load_x(r + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wA, kbA + (r + 2) * WK + wk);
+    __builtin_amdgcn_sched_barrier(0);
     compute(wB, 1);
-    if (more2) store_x(0);
+    store_x(0);
+    __syncthreads();
+  }
+  if (r < nrounds) {  // odd round count: the last round sits in wA / buffer 0
+    compute(wA, 0);
     __syncthreads();
   }
 
-  // ---- row statistics over this K-range -----------------------------------------
+// ---- row statistics over this K-range -----------------------------------------
 #pragma unroll
   for (int i = 0; i < XIT; ++i) {
     float s = sq[i];
@@ -452,17 +455,18 @@ wstream_kernel(const WsArgs a) {
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) {
           const int n = n_wave0 + u * 16 + 4 * lg;
-          *(f32x4 *)(part + ((int64_t)sp * MPAD + m) * Npad + n) = acc[t][u];
+          float *dst = part + ((int64_t)sp * MPAD + m) * Npad + n;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pub_f32(dst + j, acc[t][u][j]);
         }
       }
     }
-    if (th < MPAD) sqp[((int64_t)grp * a.S + sp) * MPAD + th] = sq_row[th];
-    __threadfence();
+    if (th < MPAD) pub_f32(sqp + ((int64_t)grp * a.S + sp) * MPAD + th, sq_row[th]);
+    wait_stores();
     __syncthreads();
-    if (th == 0) s_flag = (atomicAdd(ticket + grp, 1u) == (unsigned)(a.S - 1));
+    if (th == 0) s_flag = (ticket_add(ticket + grp) == (unsigned)(a.S - 1));
     __syncthreads();
     if (!s_flag) return;
-    __threadfence();
     constexpr int Q = NG / 4;
     for (int item = th; item < MPAD * Q; item += NT) {
       const int m = item / Q;
@@ -471,12 +475,14 @@ wstream_kernel(const WsArgs a) {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
       float ss = 0.f;
       for (int q = 0; q < a.S; ++q) {
-        s += *(const f32x4 *)(part + ((int64_t)q * MPAD + m) * Npad + n);
-        ss += sqp[((int64_t)grp * a.S + q) * MPAD + m];
+        const float *src = part + ((int64_t)q * MPAD + m) * Npad + n;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] += get_f32(src + j);
+        ss += get_f32(sqp + ((int64_t)grp * a.S + q) * MPAD + m);
       }
       finish(m, n, s, ss);
     }
-    if (th == 0) ticket[grp] = 0u;
+    if (th == 0) ticket_reset(ticket + grp);
   } else {
     // ---- EPI_ARGMAX (S == 1): per-row (max, lowest index) over the group ----
     if (wk == 0) {
@@ -525,23 +531,22 @@ wstream_kernel(const WsArgs a) {
           bv = s_bval[q][th];
           bi = s_bidx[q][th];
         }
-      pv[(int64_t)grp * MPAD + th] = bv;
-      pi[(int64_t)grp * MPAD + th] = bi;
+      pub_f32(pv + (int64_t)grp * MPAD + th, bv);
+      pub_i32(pi + (int64_t)grp * MPAD + th, bi);
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
     unsigned *ticket = a.ticket + mchunk;
-    if (th == 0) s_flag = (atomicAdd(ticket, 1u) == (unsigned)(a.G - 1));
+    if (th == 0) s_flag = (ticket_add(ticket) == (unsigned)(a.G - 1));
     __syncthreads();
     if (!s_flag) return;
-    __threadfence();
     // Final argmax over all groups: wave w handles rows w, w + waves, ...
     for (int m = wave; m < Mloc; m += WN * WK) {
       float bv = -__builtin_inff();
       int bi = 0x7fffffff;
       for (int gq = lane; gq < a.G; gq += 64) {
-        const float v = pv[(int64_t)gq * MPAD + m];
-        const int ix = pi[(int64_t)gq * MPAD + m];
+        const float v = get_f32(pv + (int64_t)gq * MPAD + m);
+        const int ix = get_i32(pi + (int64_t)gq * MPAD + m);
         if (argmax_better(v, ix, bv, bi)) {
           bv = v;
           bi = ix;
@@ -579,7 +584,7 @@ wstream_kernel(const WsArgs a) {
         a.accepted_n[b] = n;
       }
     }
-    if (th == 0) *ticket = 0u;
+    if (th == 0) ticket_reset(ticket);
   }
 }
 

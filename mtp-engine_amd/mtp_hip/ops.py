@@ -43,7 +43,7 @@ def rmsnorm_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
         bias = bias.contiguous()
         assert bias.numel() == N, f"fused_rmsnorm_linear: bias has {bias.numel()} != {N}"
     if gamma is not None:
-        gamma = gamma.contiguous()
+        gamma = gamma.contiguous().to(torch.float32)
         assert gamma.numel() == K, f"fused_rmsnorm_linear: gamma has {gamma.numel()} != {K}"
     _on_device("x", x, weight=weight, bias=bias, gamma=gamma)
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
@@ -76,7 +76,7 @@ def rmsnorm_linear_fp8(x: torch.Tensor, weight_fp8: torch.Tensor, wscale: torch.
         bias = bias.contiguous()
         assert bias.numel() == N, f"fused_rmsnorm_linear_fp8: bias has {bias.numel()} != {N}"
     if gamma is not None:
-        gamma = gamma.contiguous()
+        gamma = gamma.contiguous().to(torch.float32)
         assert gamma.numel() == K, f"fused_rmsnorm_linear_fp8: gamma has {gamma.numel()} != {K}"
     _on_device("x", x, weight=weight_fp8, wscale=wscale, bias=bias, gamma=gamma)
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
