@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <atomic>
 #include <cstring>
 
 #include "generic.hpp"
@@ -163,52 +164,81 @@ int launch_ws(const Plan &p, WsArgs &a, int epi, void *ws, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// x-resident linear kernel: plan and launch.
-constexpr size_t kLdsXBudget = 144 * 1024;  // resident x per workgroup
-constexpr size_t kLdsMax = 150 * 1024;      // dynamic LDS limit we allow
-constexpr int kWsxMinBlocks = 200;           // aim for most of the 256 CUs busy
+// Pipelined linear kernel: plan and launch.
+constexpr size_t kLdsMax = 150 * 1024;  // dynamic LDS limit we allow
+constexpr int kWspMinBlocks = 200;      // aim for most of the 256 CUs busy
 
 struct PlanX {
   bool ok = false;
   int ct = 0, wt = 0, mt = 0, variant = 0;
-  Variant var{};
-  int NG = 0, KB = 0, G = 0, S = 1, kb_per = 0, nkb = 0;
-  int rows_per_chunk = 64, chunks = 0, xcd_map = 0;
+  bool gam = false;
+  WspVariant var{};
+  int NG = 0, G = 0, S = 1, kb_per = 0, nkb = 0;
+  int chunks = 0, xcd_map = 0;
   size_t lds = 0, part_off = 0, sqp_off = 0, total = 0;
 };
 
-PlanX make_plan_x(int ct, int wt, int64_t M, int64_t N, int64_t K) {
+// Default tile variant per row count: up to 32 rows (<= 4 x blocks of a
+// unit) 64 columns per workgroup without K-splits on large N; 64 rows split
+// 128 columns over two K-halves so x loads stay <= W loads per wave.
+int wsp_default_variant(int rows) { return rows <= 32 ? 0 : 1; }
+
+// A kernel that would keep registers in scratch memory is not used: its
+// launches cost orders of magnitude more than the register-resident
+// variants. Queried once per (dtypes, tiles, variant, gamma).
+bool wsp_usable(int ct, int wt, int mt, int v, bool gam) {
+  // 0: not queried yet, 1: usable, 2: not usable (static storage starts at 0)
+  static std::atomic<signed char> cache[3][2][4][kWspNumVar][2];
+  const int ci = ct == MTP_BF16 ? 0 : ct == MTP_F16 ? 1 : 2;
+  std::atomic<signed char> &c = cache[ci][wt == MTP_FP8E4M3][mt - 1][v][gam];
+  signed char s = c.load(std::memory_order_relaxed);
+  if (s == 0) {
+    WsKernel k = wsp_pick_kernel(ct, wt, mt, v, gam);
+    hipFuncAttributes fa{};
+    // without a device the attributes are unknown; the launch reports errors
+    const bool ok =
+        k && (hipFuncGetAttributes(&fa, (const void *)k) != hipSuccess || fa.localSizeBytes == 0);
+    s = ok ? 1 : 2;
+    c.store(s, std::memory_order_relaxed);
+  }
+  return s == 1;
+}
+
+PlanX make_plan_x(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   PlanX p;
   p.ct = ct;
   p.wt = wt;
+  p.gam = gam;
   const int cb = dtype_bytes(ct), wb = dtype_bytes(wt);
   if (!fast_pair(ct, wt) || M <= 0 || N <= 0 || K <= 0) return p;
-  if (K % (16 / cb) != 0 || K % (16 / wb) != 0) return p;
+  // whole 64-byte units per W row (and so whole 16-byte x fragments)
+  if ((K * wb) % 64 != 0) return p;
+  // buffer descriptors span one column group of W and one row chunk of x;
+  // both stay below the out-of-range offset 2^31
   if ((int64_t)256 * K * wb >= (int64_t)1 << 31 || (int64_t)64 * K * cb >= (int64_t)1 << 31)
     return p;
   p.chunks = (int)((M + 63) / 64);
   const int rows = (int)(M < 64 ? M : 64);
   p.mt = (rows + 15) / 16;
-  int variant = rows <= 16 ? 0 : 1, splits = -1;
+  int variant = wsp_default_variant(rows), splits = -1;
   tune_override(variant, splits);
-  if (variant >= kWsxNumVar) variant = 0;
+  if (variant >= kWspNumVar) variant = 0;
+  if (!wsp_usable(ct, wt, p.mt, variant, gam)) variant = 1;
+  if (!wsp_usable(ct, wt, p.mt, variant, gam)) return p;
   p.variant = variant;
-  p.var = wsx_variant(ct, wt, variant);
-  const int LG = p.var.wbl / wb;
-  p.KB = 4 * LG;
+  p.var = kWspVar[variant];
+  const int KU = 64 / wb;                 // k per unit (64 bytes of a W row)
+  const int H = (16 / wb) / (16 / cb);    // x fragments per W lane chunk
   p.NG = p.var.wn * p.var.nsub * 16;
   p.G = (int)((N + p.NG - 1) / p.NG);
-  p.nkb = (int)((K + p.KB - 1) / p.KB);
-  const int MPAD = p.mt * 16;
-  const size_t blk = (size_t)MPAD * p.KB * cb;
-  const int kb_max = (int)(kLdsXBudget / blk);
-  if (kb_max < 1) return p;
-  int S = (p.nkb + kb_max - 1) / kb_max;
+  p.nkb = (int)((K + KU - 1) / KU);
+  int S = 1;
   if (splits > 0) {
-    S = splits > S ? splits : S;
+    S = splits;
   } else {
-    // more K-splits while the grid is short of CUs and every wave keeps >= 2 K-blocks
-    while ((int64_t)p.G * S * p.chunks < kWsxMinBlocks && p.nkb / (S + 1) >= 2 * p.var.wk) ++S;
+    // more K-splits while the grid is short of CUs and every K-group keeps
+    // >= 4 stages
+    while ((int64_t)p.G * S * p.chunks < kWspMinBlocks && p.nkb / (S + 1) >= 4 * p.var.wk) ++S;
   }
   if (S > p.nkb) S = p.nkb;
   if (S > 1 && (int64_t)p.chunks * p.G > kCounterSlots) return p;
@@ -216,11 +246,14 @@ PlanX make_plan_x(int ct, int wt, int64_t M, int64_t N, int64_t K) {
   p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
   const int total = p.G * p.S;
   p.xcd_map = (total % 8 == 0 && (total / 8) % p.S == 0) ? 1 : 0;
-  // the all-wave reduction parks every wave's accumulators in the x region
-  const size_t red = (size_t)p.var.wk * p.var.wn * 64 * p.mt * p.var.nsub * 16;
-  p.lds = (size_t)p.kb_per * blk;
-  if (red > p.lds) p.lds = red;
+  const int64_t upg = (p.kb_per + p.var.wk - 1) / p.var.wk;
+  const int nt = p.var.wn * p.var.wk * 64;
+  // gamma of the K-range (plus one padding unit) is staged by kWspGJ 16-byte
+  // loads per thread
+  if (gam && (p.var.wk * upg + 1) * KU / 4 > (int64_t)kWspGJ * nt) return p;
+  p.lds = wsp_lds_bytes(p.mt, H, p.var.nsub, p.var.wn, p.var.wk, upg, KU, gam);
   if (p.lds > kLdsMax) return p;
+  const int MPAD = p.mt * 16;
   const int64_t Npad = (int64_t)p.G * p.NG;
   // split-K partials of one row chunk sit behind one buffer descriptor
   if (p.S > 1 && (int64_t)p.S * MPAD * Npad * 4 >= (int64_t)1 << 31) return p;
@@ -237,8 +270,8 @@ PlanX make_plan_x(int ct, int wt, int64_t M, int64_t N, int64_t K) {
   return p;
 }
 
-int launch_wsx(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
-  WsKernel k = wsx_pick_kernel(p.ct, p.wt, p.mt, p.variant);
+int launch_wsp(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
+  WsKernel k = wsp_pick_kernel(p.ct, p.wt, p.mt, p.variant, p.gam);
   if (!k) return MTP_ERR_DTYPE;
   unsigned char *w8 = (unsigned char *)ws;
   a.rows_per_chunk = 64;
@@ -291,7 +324,7 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   if (!x && K > 0) return MTP_ERR_NULL;
   if ((!w && K > 0) || !y) return MTP_ERR_NULL;
   hipStream_t st = (hipStream_t)stream;
-  PlanX p = make_plan_x(xt, wt, M, N, K);
+  PlanX p = make_plan_x(xt, wt, M, N, K, gamma != nullptr);
   const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!gamma || aligned16(gamma));
   // the tiled kernel reads gamma as fp32 (the Python shim upcasts it)
   if (!p.ok || !aligned || (gamma && gt != MTP_F32)) {
@@ -313,7 +346,7 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
-  return launch_wsx(p, a, ws, st);
+  return launch_wsp(p, a, ws, st);
 }
 
 }  // namespace
@@ -342,8 +375,13 @@ const char *mtp_last_hip_error(void) { return g_last_hip_error; }
 size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, int64_t N,
                                           int64_t K) {
   if (w_kind == MTP_U8) return 0;  // packed INT4: no split-K workspace yet
-  PlanX p = make_plan_x(x_dtype, w_kind, M, N, K);
-  return p.ok ? p.total : 0;
+  // enough for the call with or without gamma
+  size_t most = 0;
+  for (int gam = 0; gam < 2; ++gam) {
+    PlanX p = make_plan_x(x_dtype, w_kind, M, N, K, gam != 0);
+    if (p.ok && p.total > most) most = p.total;
+  }
+  return most;
 }
 
 int mtp_fused_rmsnorm_linear(const void *x, int x_dtype, int64_t M, int64_t K, const void *weight,

@@ -1,6 +1,7 @@
-// Tile variants of the weight-streaming kernel and their dispatch. The
-// instantiations live in one translation unit per compute type
-// (ws_bf16.hip, ws_f16.hip, ws_f32.hip) so they compile in parallel.
+// Tile variants of the weight-streaming kernels and their dispatch. The
+// instantiations live in one translation unit per compute type (verify:
+// ws_bf16.hip, ws_f16.hip, ws_f32.hip) or per dtype pair (linear:
+// wsp_<ct>_<wt>.hip) so they compile in parallel.
 //
 // A wave keeps at most NSUB * WBL / 16 <= 8 sixteen-byte W loads per K-block
 // in flight (double-buffered: <= 16 outstanding): on gfx950 waves with more
@@ -8,8 +9,8 @@
 // bytes in flight per CU come from more waves instead.
 #pragma once
 
+#include "wsp.hpp"
 #include "wstream.hpp"
-#include "wsx.hpp"
 
 namespace mtp {
 
@@ -77,62 +78,75 @@ WsKernel ws_pick(int mt, int v) {
   return nullptr;
 }
 
-// ---- x-resident linear kernel (wsx.hpp) -----------------------------------
-constexpr WsVariant kWsxVar[] = {
-    {2, 2, 8, 64},  // 0: 1024 threads, 64 columns, 8-way K split in the workgroup
-    {2, 4, 4, 64},  // 1: 1024 threads, 128 columns
-    {2, 4, 2, 64},  // 2: 512 threads, 128 columns
-    {2, 2, 4, 64},  // 3: 512 threads, 64 columns
+// ---- pipelined linear kernel (wsp.hpp) -------------------------------------
+// {nsub, wn, wk}: a wave covers 16 * nsub columns, wn waves share one x ring
+// per K-group, wk K-groups per workgroup.
+struct WspVariant {
+  int nsub, wn, wk;
 };
-constexpr int kWsxNumVar = 4;
+constexpr WspVariant kWspVar[] = {
+    {2, 2, 8},  // 0: 1024 threads, 64 columns
+    {2, 4, 4},  // 1: 1024 threads, 128 columns
+    {2, 8, 2},  // 2: 1024 threads, 256 columns
+    {2, 4, 2},  // 3: 512 threads, 128 columns
+    {2, 2, 4},  // 4: 512 threads, 64 columns
+    {4, 2, 4},  // 5: 512 threads, 128 columns, 64 columns per wave
+    {1, 4, 4},  // 6: 1024 threads, 64 columns, 16 columns per wave
+    {4, 4, 2},  // 7: 512 threads, 256 columns, 64 columns per wave
+};
+constexpr int kWspNumVar = 8;
 
-// fp32 activations with fp8 weights use 32-byte lane runs (K-block of 128).
-constexpr WsVariant wsx_effective(int ct, int wt, WsVariant v) {
-  if (ct == MTP_F32 && wt == MTP_FP8E4M3) return WsVariant{v.nsub, v.wn, v.wk, 32};
-  return v;
+template <int CT, int WT, int MT, int I, bool GAM>
+WsKernel wsp_inst() {
+  constexpr WspVariant v = kWspVar[I];
+  return wsp_kernel<CT, WT, MT, v.nsub, v.wn, v.wk, GAM>;
 }
-inline WsVariant wsx_variant(int ct, int wt, int v) { return wsx_effective(ct, wt, kWsxVar[v]); }
 
-template <int CT, int WT, int MT, int I>
-WsKernel wsx_inst() {
-  constexpr WsVariant v = wsx_effective(CT, WT, kWsxVar[I]);
-  return wsx_kernel<CT, WT, MT, v.nsub, v.wn, v.wk, v.wbl>;
-}
-
-template <int CT, int WT>
-WsKernel wsx_pick(int mt, int v) {
-#define MTP_WSX_CASES(MT)                   \
-  switch (v) {                              \
-    case 0: return wsx_inst<CT, WT, MT, 0>(); \
-    case 1: return wsx_inst<CT, WT, MT, 1>(); \
-    case 2: return wsx_inst<CT, WT, MT, 2>(); \
-    case 3: return wsx_inst<CT, WT, MT, 3>(); \
-  }                                         \
+template <int CT, int WT, bool GAM>
+WsKernel wsp_pick(int mt, int v) {
+#define MTP_WSP_CASES(MT)                          \
+  switch (v) {                                     \
+    case 0: return wsp_inst<CT, WT, MT, 0, GAM>(); \
+    case 1: return wsp_inst<CT, WT, MT, 1, GAM>(); \
+    case 2: return wsp_inst<CT, WT, MT, 2, GAM>(); \
+    case 3: return wsp_inst<CT, WT, MT, 3, GAM>(); \
+    case 4: return wsp_inst<CT, WT, MT, 4, GAM>(); \
+    case 5: return wsp_inst<CT, WT, MT, 5, GAM>(); \
+    case 6: return wsp_inst<CT, WT, MT, 6, GAM>(); \
+    case 7: return wsp_inst<CT, WT, MT, 7, GAM>(); \
+  }                                                \
   return nullptr;
   switch (mt) {
-    case 1: { MTP_WSX_CASES(1) }
-    case 2: { MTP_WSX_CASES(2) }
-    case 3: { MTP_WSX_CASES(3) }
-    case 4: { MTP_WSX_CASES(4) }
+    case 1: { MTP_WSP_CASES(1) }
+    case 2: { MTP_WSP_CASES(2) }
+    case 3: { MTP_WSP_CASES(3) }
+    case 4: { MTP_WSP_CASES(4) }
   }
-#undef MTP_WSX_CASES
+#undef MTP_WSP_CASES
   return nullptr;
 }
 
-// Defined in ws_<ct>.hip: the kernel for (weight type, M tiles, variant,
-// epilogue) at that compute type, or null if not instantiated.
+// Defined in ws_<ct>.hip: the verify (argmax) kernel at that compute type for
+// (M tiles, variant), or null if not instantiated.
 WsKernel ws_pick_bf16(int wt, int mt, int v, int epi);
 WsKernel ws_pick_f16(int wt, int mt, int v, int epi);
 WsKernel ws_pick_f32(int wt, int mt, int v, int epi);
-WsKernel wsx_pick_bf16(int wt, int mt, int v);
-WsKernel wsx_pick_f16(int wt, int mt, int v);
-WsKernel wsx_pick_f32(int wt, int mt, int v);
+// Defined in wsp_<ct>_<wt>.hip: the linear kernel for (M tiles, variant,
+// gamma present).
+WsKernel wsp_pick_bf16_bf16(int mt, int v, bool gam);
+WsKernel wsp_pick_bf16_fp8(int mt, int v, bool gam);
+WsKernel wsp_pick_f16_f16(int mt, int v, bool gam);
+WsKernel wsp_pick_f16_fp8(int mt, int v, bool gam);
+WsKernel wsp_pick_f32_f32(int mt, int v, bool gam);
+WsKernel wsp_pick_f32_fp8(int mt, int v, bool gam);
 
-inline WsKernel wsx_pick_kernel(int ct, int wt, int mt, int v) {
+inline WsKernel wsp_pick_kernel(int ct, int wt, int mt, int v, bool gam) {
+  const bool f8 = wt == MTP_FP8E4M3;
+  if (!f8 && wt != ct) return nullptr;
   switch (ct) {
-    case MTP_BF16: return wsx_pick_bf16(wt, mt, v);
-    case MTP_F16: return wsx_pick_f16(wt, mt, v);
-    case MTP_F32: return wsx_pick_f32(wt, mt, v);
+    case MTP_BF16: return f8 ? wsp_pick_bf16_fp8(mt, v, gam) : wsp_pick_bf16_bf16(mt, v, gam);
+    case MTP_F16: return f8 ? wsp_pick_f16_fp8(mt, v, gam) : wsp_pick_f16_f16(mt, v, gam);
+    case MTP_F32: return f8 ? wsp_pick_f32_fp8(mt, v, gam) : wsp_pick_f32_f32(mt, v, gam);
   }
   return nullptr;
 }

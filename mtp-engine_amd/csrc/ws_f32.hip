@@ -1,25 +1,11 @@
-// Instantiations of the weight-streaming kernel at compute type F32.
+// Instantiations of the verify (argmax) weight-streaming kernel at compute
+// type F32.
 #include "ws_dispatch.hpp"
 
 namespace mtp {
 
 WsKernel ws_pick_f32(int wt, int mt, int v, int epi) {
-  if (epi == EPI_LINEAR) {
-    if (wt == MTP_F32) return ws_pick<MTP_F32, MTP_F32, EPI_LINEAR>(mt, v);
-    if (wt == MTP_FP8E4M3) return ws_pick<MTP_F32, MTP_FP8E4M3, EPI_LINEAR>(mt, v);
-  } else {
-    if (wt == MTP_F32) return ws_pick<MTP_F32, MTP_F32, EPI_ARGMAX>(mt, v);
-  }
-  return nullptr;
-}
-
-}  // namespace mtp
-
-namespace mtp {
-
-WsKernel wsx_pick_f32(int wt, int mt, int v) {
-  if (wt == MTP_F32) return wsx_pick<MTP_F32, MTP_F32>(mt, v);
-  if (wt == MTP_FP8E4M3) return wsx_pick<MTP_F32, MTP_FP8E4M3>(mt, v);
+  if (epi == EPI_ARGMAX && wt == MTP_F32) return ws_pick<MTP_F32, MTP_F32, EPI_ARGMAX>(mt, v);
   return nullptr;
 }
 

@@ -57,7 +57,8 @@ def test_rmsnorm_linear_matches_oracle(dtype, M, N, K):
     assert ok, f"worst err/bound = {worst:.3g}"
 
 
-@pytest.mark.parametrize("tune", ["0,1", "0,3", "1,1", "1,4", "2,2", "3,5", "3,1"])
+@pytest.mark.parametrize("tune", ["0,1", "0,3", "1,1", "1,4", "2,2", "3,5", "4,1", "5,2",
+                                  "6,3", "7,1", "7,4"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_tile_variants_and_splits(tune, dtype):
     from mtp_hip import ops
@@ -118,6 +119,28 @@ def test_fp8_weights_match_oracle(M, N, K, xdtype):
     print(f"case fp8 M={M} N={N} K={K} x={xdtype}", flush=True)
     y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
     ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+    ok, worst = close(y, ref, RTOL[xdtype])
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("tune", ["0,1", "1,2", "2,3", "3,1", "4,2", "5,1", "6,2", "7,3"])
+@pytest.mark.parametrize("M", [40, 64])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float32])
+def test_fp8_tile_variants_and_splits(tune, M, xdtype):
+    """Every tile variant with fp8 weights: two x fragments per W chunk at
+    16-bit x (four at fp32 x), so some variants stage several x blocks per
+    wave and others leave waves without one."""
+    from mtp_hip import ops
+    os.environ["MTP_WS_TUNE"] = tune
+    N, K = 592, 1216
+    g = torch.Generator().manual_seed(M * 3 + 1)
+    W = 0.02 * torch.randn(N, K, generator=g)
+    wq, ws = O.quantize_fp8_per_channel(W)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    print(f"case fp8 tune={tune} M={M} x={xdtype}", flush=True)
+    y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), None, 1e-6, gamma=_dev(gm))
+    ref = O.rmsnorm_linear_fp8(x, wq, ws, None, 1e-6, gamma=gm)
     ok, worst = close(y, ref, RTOL[xdtype])
     assert ok, f"worst err/bound = {worst:.3g}"
 
