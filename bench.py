@@ -168,6 +168,19 @@ def make_verify_case(torch, lib, L):
     return case
 
 
+def pmc_traffic(name: str):
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
+    or None when no summary is committed."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return int(d["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline_fp8(torch, M: int):
     from mtp_hip import workloads
     from oracle import eager as O
@@ -209,6 +222,9 @@ def main():
     ap.add_argument("--all", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a 256 MiB device copy (known HBM bytes) so rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE can be scaled to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs on a single MI355X and has no "
@@ -249,6 +265,16 @@ def main():
         del case
         torch.cuda.empty_cache()
 
+    if args.copy_calib:
+        n = 256 * 2 ** 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        detail["copy_calib"] = dict(bytes_read=n, bytes_written=n, launches=5)
+        del src, dst
+
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle, fp8 M=64)")
@@ -274,7 +300,8 @@ def main():
                                "scales: x bf16 [64,4096], gamma [4096], W [14336,4096], bf16 out",
                    "M": 64, "K": 4096, "N": 14336, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": pmc_traffic("fp8_rmsnorm_linear_M64.pmc.json"),
                      "algorithmic_bytes": case.nbytes},
         "cpu_baseline": cpu,
         "detail": detail,

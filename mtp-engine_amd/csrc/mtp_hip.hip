@@ -82,7 +82,8 @@ Plan make_plan(int ct, int wt, int64_t M, int64_t N, int64_t K, int epi, int row
   p.chunks = (int)((M + rows_per_chunk - 1) / rows_per_chunk);
   const int rows = (int)(M < rows_per_chunk ? M : rows_per_chunk);
   p.mt = (rows + 15) / 16;
-  int variant = 0, splits = -1;
+  // verify: 512 columns per workgroup of 16 waves streamed the lm_head fastest
+  int variant = epi == EPI_ARGMAX ? 5 : 0, splits = -1;
   tune_override(variant, splits);
   if (variant >= num_variants(ct)) variant = 0;
   p.variant = variant;
