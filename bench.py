@@ -168,6 +168,58 @@ def make_verify_case(torch, lib, L):
     return case
 
 
+def make_tree_verify_case(torch, lib, L):
+    """Tree-verify step: 64-node attention over 2048 paged context tokens plus
+    the ancestors (one launch), then RMSNorm+linear 4096 -> 4096 bf16."""
+    import math
+    from mtp_hip import workloads
+    d = workloads.tree_verify()
+    dev = torch.device("cuda")
+    t = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    N, H, D = d["q"].shape
+    Lc = d["page_table"].shape[-1]
+    P = d["k_pages"].shape[0]
+    ps = d["page_size"]
+    tmask = t["tree_mask"].contiguous()
+    att = torch.empty_like(t["q"])
+    K = H * D
+    Nout = d["weight"].shape[0]
+    # weights and the paged KV cache both rotate past the MALL
+    nrot = rotations(min(Nout * K * 2, 2 * P * H * ps * D * 2))
+    wl = [t["weight"]] + [t["weight"].clone() for _ in range(nrot - 1)]
+    kpl = [t["k_pages"]] + [t["k_pages"].clone() for _ in range(nrot - 1)]
+    vpl = [t["v_pages"]] + [t["v_pages"].clone() for _ in range(nrot - 1)]
+    y = torch.empty((N, Nout), dtype=torch.bfloat16, device=dev)
+    na = lib.mtp_attention_workspace_bytes(L.BF16, 1, N, H, D, Lc, N)
+    nl = lib.mtp_rmsnorm_linear_workspace_bytes(L.BF16, L.BF16, N, Nout, K)
+    ws = torch.zeros(max(na, nl, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    scale = ctypes.c_float(1.0 / math.sqrt(D))
+    a_args = [(t["q"].data_ptr(), L.BF16, N, H, D, kp.data_ptr(), vp.data_ptr(), P,
+               t["page_table"].data_ptr(), Lc, ps, t["k_tree"].data_ptr(), t["v_tree"].data_ptr(),
+               tmask.data_ptr(), L.F32, scale, att.data_ptr(), ws.data_ptr(), na, stream)
+              for kp, vp in zip(kpl, vpl)]
+    l_args = [(att.data_ptr(), L.BF16, N, K, w.data_ptr(), L.BF16, Nout, None, 0, None, 0,
+               ctypes.c_float(d["eps"]), ctypes.c_float(1.0), 1, y.data_ptr(), ws.data_ptr(), nl,
+               stream) for w in wl]
+
+    def launch(i):
+        st = lib.mtp_tree_verify_attention(*a_args[i % nrot])
+        if st != 0:
+            raise RuntimeError(f"tree-verify attention failed: {st}")
+        st = lib.mtp_fused_rmsnorm_linear(*l_args[i % nrot])
+        if st != 0:
+            raise RuntimeError(f"tree-verify linear failed: {st}")
+
+    # bytes: context KV + tree KV + q + out + table + mask, then the linear
+    att_bytes = 2 * Lc * H * D * 2 + 2 * N * H * D * 2 + 2 * N * H * D * 2 + Lc * 4 + N * N * 4
+    lin_bytes = N * K * 2 + Nout * K * 2 + N * Nout * 2
+    flops = 4 * H * D * (N * Lc + int(d["tree_mask"].sum())) + 2 * N * Nout * K
+    case = Case("tree_verify_step_64nodes_ctx2048", launch, att_bytes + lin_bytes, flops, "hbm", nrot)
+    case.keep = (t, tmask, att, wl, kpl, vpl, y, ws)
+    return case
+
+
 def pmc_traffic(name: str):
     """HBM bytes per launch of the headline kernel from the committed rocprofv3
     --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
@@ -243,7 +295,8 @@ def main():
         builders += [("fp8_M8", lambda: make_fp8_case(torch, lib, L, 8)),
                      ("fp8_M32", lambda: make_fp8_case(torch, lib, L, 32)),
                      ("fp32_M16", lambda: make_fp32_case(torch, lib, L)),
-                     ("multi_verify", lambda: make_verify_case(torch, lib, L))]
+                     ("multi_verify", lambda: make_verify_case(torch, lib, L)),
+                     ("tree_verify", lambda: make_tree_verify_case(torch, lib, L))]
     if args.only:
         builders = [b for b in builders if b[0] in args.only.split(",")]
     for key, mk in builders:

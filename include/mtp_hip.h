@@ -182,6 +182,71 @@ int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B,
 size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq,
                                   int64_t V, int64_t K);
 
+/* ------------------------------------------------------------------------- */
+/* Tree / paged attention                                                    */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Replaces fused_paged_attention(q, k_pages, v_pages, page_table, page_size,
+ * scale=None) (mtp_kernels.py:1136-1162; kernel 494-554; eager 832-856):
+ *   out[b, h] = softmax_t(q[b, h] . k_t * scale) @ v_t,
+ *   k_t = k_pages[page_table[b, t], b, h, t % page_size]   (t < L)
+ * q / out [B, H, D]; k_pages / v_pages [num_pages, B, H, page_size, D]; all
+ * in dtype (F32, BF16, F16); page_table [B, L] int32 (the reference casts it,
+ * 1143). scale: the caller passes 1/sqrt(D) for the reference default. A
+ * page index outside [0, num_pages) masks its key instead of being read.
+ */
+int mtp_fused_paged_attention(const void *q, int dtype, int64_t B, int64_t H,
+                              int64_t D, const void *k_pages,
+                              const void *v_pages, int64_t num_pages,
+                              const int32_t *page_table, int64_t L,
+                              int64_t page_size, float scale, void *out,
+                              void *workspace, size_t workspace_bytes,
+                              void *stream);
+
+/*
+ * Replaces fused_tree_attention(q, k, v, mask, scale=None)
+ * (mtp_kernels.py:1165-1191; kernel 559-613; eager 859-872):
+ *   out[b, h] = softmax_l(where(mask[l] > 0.5, q[b, h] . k[b, h, l] * scale,
+ *               -inf)) @ v[b, h, l]      (every key masked: NaN, as there)
+ * q / out [B, H, D]; k / v [B, H, L, D]; mask [L] in mask_dtype (F32, BF16,
+ * F16, or U8 for bool).
+ */
+int mtp_fused_tree_attention(const void *q, int dtype, int64_t B, int64_t H,
+                             int64_t D, const void *k, const void *v, int64_t L,
+                             const void *mask, int mask_dtype, float scale,
+                             void *out, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
+/*
+ * The tree-verify attention step in one launch (no single reference
+ * function: the reference composes it from one fused_tree_attention call per
+ * node over keys = context ++ tree nodes, mtp_kernels.py:1165-1191, with the
+ * SpeculativeDraftTree mask, mtp_engine.py:671-680):
+ *   out[n, h] = softmax over { context tokens t < Lc } u { tree nodes m with
+ *               tree_mask[n, m] > 0.5 } of q[n, h] . k * scale, @ v
+ * q_nodes / k_tree / v_tree / out [N, H, D]; k_pages / v_pages
+ * [num_pages, 1, H, page_size, D]; page_table [1, Lc] int32; tree_mask
+ * [N, N] in mask_dtype.
+ */
+int mtp_tree_verify_attention(const void *q_nodes, int dtype, int64_t N,
+                              int64_t H, int64_t D, const void *k_pages,
+                              const void *v_pages, int64_t num_pages,
+                              const int32_t *page_table, int64_t Lc,
+                              int64_t page_size, const void *k_tree,
+                              const void *v_tree, const void *tree_mask,
+                              int mask_dtype, float scale, void *out,
+                              void *workspace, size_t workspace_bytes,
+                              void *stream);
+
+/* Workspace bytes for the attention entry points: B batch rows, NQ queries
+ * per (batch, head) (1 for the two reference functions, N for tree verify),
+ * Lc context keys, Lt dense keys (L of fused_tree_attention, N of tree
+ * verify). */
+size_t mtp_attention_workspace_bytes(int dtype, int64_t B, int64_t NQ,
+                                     int64_t H, int64_t D, int64_t Lc,
+                                     int64_t Lt);
+
 #ifdef __cplusplus
 }
 #endif

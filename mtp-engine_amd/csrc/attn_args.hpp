@@ -1,0 +1,40 @@
+// Launch arguments of the attention kernels (attn.hpp), shared with the
+// host code that plans them.
+#pragma once
+
+#include <stdint.h>
+
+namespace mtp {
+
+constexpr int kAttnMaxChunks = 32;  // context chunks per (b, h)
+
+struct AttnArgs {
+  const void *q;               // element strides: batch, query, head (d stride 1)
+  int64_t q_sb, q_sn, q_sh;
+  const void *kp, *vp;         // pages [P, B, H, page_size, D] or null (Lc == 0)
+  const int32_t *table;        // [B, ld_tab] physical page of each context key
+  int64_t ld_tab;
+  int Lc, page_size, npages;
+  int64_t p_sp, p_sb, p_sh;    // page element strides: page, batch, head
+  const void *kd, *vd;         // dense keys or null (Lt == 0)
+  int Lt;
+  int64_t d_sb, d_sh, d_st;    // dense element strides: batch, head, key
+  const void *mask;            // null, [Lt] or [NQ, Lt]
+  int mask_dt, mask_2d;
+  void *out;                   // element strides: batch, query, head
+  int64_t o_sb, o_sn, o_sh;
+  int B, NQ, H;
+  float scale;
+  int nchunks, chunk_blocks;   // context blocks of 32 keys per chunk
+  float *part;                 // [B*H][nchunks][16*QT][D]
+  float *ml;                   // [B*H][nchunks][16*QT][2]
+  unsigned *ticket;            // [B*H]
+};
+
+typedef void (*AttnKernel)(AttnArgs);
+// Defined in attn.hip: the MFMA kernel for (compute type, head dim, query
+// tiles of 16) or null, and the fallback kernel.
+AttnKernel attn_pick(int ct, int d, int qt);
+void (*attn_generic())(AttnArgs, int, int);
+
+}  // namespace mtp

@@ -4,9 +4,11 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 
+#include "attn_args.hpp"
 #include "generic.hpp"
 #include "ws_dispatch.hpp"
 
@@ -350,6 +352,80 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   return launch_wsp(p, a, ws, st);
 }
 
+
+// ---------------------------------------------------------------------------
+// Attention: plan and launch.
+constexpr int kAttnTargetBlocks = 256;  // one workgroup per CU
+
+struct AttnPlan {
+  int qt = 0, nchunks = 1, chunk_blocks = 0;
+  bool fast = false;
+  size_t part_off = 0, ml_off = 0, total = 0;
+};
+
+AttnPlan make_attn_plan(int ct, int64_t B, int64_t NQ, int64_t H, int64_t D, int64_t Lc,
+                        int64_t Lt) {
+  AttnPlan p;
+  p.fast = (ct == MTP_BF16 || ct == MTP_F16) && (D == 64 || D == 128) && NQ >= 1 && NQ <= 64;
+  const int64_t nctx_blocks = (Lc + 31) / 32;
+  if (!p.fast) return p;  // the fallback needs no workspace
+  p.qt = (int)((NQ + 15) / 16);
+  int nch = 1;
+  if (nctx_blocks > 0) {
+    const int64_t want = (kAttnTargetBlocks + B * H - 1) / (B * H);
+    nch = (int)std::min<int64_t>(std::max<int64_t>(want, 1), nctx_blocks);
+    nch = std::min(nch, kAttnMaxChunks);
+  }
+  p.chunk_blocks = nctx_blocks > 0 ? (int)((nctx_blocks + nch - 1) / nch) : 0;
+  p.nchunks = nctx_blocks > 0 ? (int)((nctx_blocks + p.chunk_blocks - 1) / p.chunk_blocks) : 1;
+  if (p.nchunks > 1) {
+    const int64_t qp = (int64_t)p.qt * 16;
+    size_t off = kCounterBytes;
+    p.part_off = off;
+    off += align_up((size_t)(B * H) * p.nchunks * qp * D * 4, 256);
+    p.ml_off = off;
+    off += align_up((size_t)(B * H) * p.nchunks * qp * 2 * 4, 256);
+    p.total = off;
+  }
+  return p;
+}
+
+// Shared launch path of the three attention entry points. All strides are
+// in elements; the MFMA kernel needs 16-byte aligned rows (strides multiple
+// of 8 elements), the fallback takes anything.
+int launch_attention(AttnArgs &a, int ct, int64_t D, void *ws, size_t ws_bytes, hipStream_t st) {
+  if (a.B * (int64_t)a.H > INT32_MAX || a.NQ > 65535) return MTP_ERR_SHAPE;
+  AttnPlan p = make_attn_plan(ct, a.B, a.NQ, a.H, D, a.Lc, a.Lt);
+  const bool strides8 = (a.q_sb | a.q_sn | a.q_sh | a.p_sp | a.p_sb | a.p_sh | a.d_sb | a.d_sh |
+                         a.d_st | a.o_sb | a.o_sn | a.o_sh) % 8 == 0;
+  const bool aligned = aligned16(a.q) && aligned16(a.out) && (!a.kp || aligned16(a.kp)) &&
+                       (!a.vp || aligned16(a.vp)) && (!a.kd || aligned16(a.kd)) &&
+                       (!a.vd || aligned16(a.vd));
+  if (p.fast && strides8 && aligned) {
+    if (p.total > 0 && (!ws || ws_bytes < p.total)) return MTP_ERR_WORKSPACE;
+    if (p.nchunks > 1 && (int64_t)a.B * a.H > kCounterSlots) return MTP_ERR_SHAPE;
+    AttnKernel k = attn_pick(ct, (int)D, p.qt);
+    if (!k) return MTP_ERR_DTYPE;
+    unsigned char *w8 = (unsigned char *)ws;
+    a.nchunks = p.nchunks;
+    a.chunk_blocks = p.chunk_blocks;
+    if (p.nchunks > 1) {
+      a.part = (float *)(w8 + p.part_off);
+      a.ml = (float *)(w8 + p.ml_off);
+      a.ticket = (unsigned *)w8;
+    }
+    dim3 grid((unsigned)(a.B * a.H), (unsigned)p.nchunks, 1);
+    hipLaunchKernelGGL(k, grid, dim3(p.qt * 64), 0, st, a);
+    return launch_status();
+  }
+  if (D > 256) return MTP_ERR_SHAPE;
+  dim3 grid((unsigned)(a.B * a.H), (unsigned)a.NQ, 1);
+  hipLaunchKernelGGL(attn_generic(), grid, dim3(64), 0, st, a, (int)D, ct);
+  return launch_status();
+}
+
+bool mask_dt_ok(int dt) { return is_float_dt(dt) || dt == MTP_U8; }
+
 }  // namespace
 
 // ===========================================================================
@@ -498,6 +574,130 @@ int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B, int64_t S
   const int rpc = verify_rows_per_chunk(S);
   return verify_common(hidden, h_dtype, B * S, K, weight, w_dtype, V, bias, bias_dtype, rpc, a,
                        workspace, workspace_bytes, stream);
+}
+
+
+size_t mtp_attention_workspace_bytes(int dtype, int64_t B, int64_t NQ, int64_t H, int64_t D,
+                                     int64_t Lc, int64_t Lt) {
+  if (B <= 0 || NQ <= 0 || H <= 0 || D <= 0 || Lc < 0 || Lt < 0) return 0;
+  return make_attn_plan(dtype, B, NQ, H, D, Lc, Lt).total;
+}
+
+int mtp_fused_paged_attention(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                              const void *k_pages, const void *v_pages, int64_t num_pages,
+                              const int32_t *page_table, int64_t L, int64_t page_size,
+                              float scale, void *out, void *workspace, size_t workspace_bytes,
+                              void *stream) {
+  if (!is_float_dt(dtype)) return MTP_ERR_DTYPE;
+  if (B < 0 || H < 0 || D <= 0 || L < 0 || page_size <= 0 || num_pages < 0 || L > INT32_MAX ||
+      num_pages > INT32_MAX || page_size > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (B == 0 || H == 0) return MTP_OK;
+  if (!q || !out || (L > 0 && (!k_pages || !v_pages || !page_table))) return MTP_ERR_NULL;
+  if (L > 0 && num_pages == 0) return MTP_ERR_SHAPE;
+  AttnArgs a{};
+  a.q = q;
+  a.q_sb = H * D;
+  a.q_sn = 0;
+  a.q_sh = D;
+  a.kp = k_pages;
+  a.vp = v_pages;
+  a.table = page_table;
+  a.ld_tab = L;
+  a.Lc = (int)L;
+  a.page_size = (int)page_size;
+  a.npages = (int)num_pages;
+  a.p_sh = page_size * D;
+  a.p_sb = H * a.p_sh;
+  a.p_sp = B * a.p_sb;
+  a.out = out;
+  a.o_sb = H * D;
+  a.o_sn = 0;
+  a.o_sh = D;
+  a.B = (int)B;
+  a.NQ = 1;
+  a.H = (int)H;
+  a.scale = scale;
+  return launch_attention(a, dtype, D, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mtp_fused_tree_attention(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                             const void *k, const void *v, int64_t L, const void *mask,
+                             int mask_dtype, float scale, void *out, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  if (!is_float_dt(dtype)) return MTP_ERR_DTYPE;
+  if (mask && !mask_dt_ok(mask_dtype)) return MTP_ERR_DTYPE;
+  if (B < 0 || H < 0 || D <= 0 || L < 0 || L > INT32_MAX) return MTP_ERR_SHAPE;
+  if (B == 0 || H == 0) return MTP_OK;
+  if (!q || !out || (L > 0 && (!k || !v || !mask))) return MTP_ERR_NULL;
+  AttnArgs a{};
+  a.q = q;
+  a.q_sb = H * D;
+  a.q_sh = D;
+  a.kd = k;
+  a.vd = v;
+  a.Lt = (int)L;
+  a.d_st = D;
+  a.d_sh = L * D;
+  a.d_sb = H * a.d_sh;
+  a.mask = mask;
+  a.mask_dt = mask_dtype;
+  a.mask_2d = 0;
+  a.out = out;
+  a.o_sb = H * D;
+  a.o_sh = D;
+  a.B = (int)B;
+  a.NQ = 1;
+  a.H = (int)H;
+  a.scale = scale;
+  return launch_attention(a, dtype, D, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mtp_tree_verify_attention(const void *q_nodes, int dtype, int64_t N, int64_t H, int64_t D,
+                              const void *k_pages, const void *v_pages, int64_t num_pages,
+                              const int32_t *page_table, int64_t Lc, int64_t page_size,
+                              const void *k_tree, const void *v_tree, const void *tree_mask,
+                              int mask_dtype, float scale, void *out, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+  if (!is_float_dt(dtype) || !mask_dt_ok(mask_dtype)) return MTP_ERR_DTYPE;
+  if (N < 0 || H < 0 || D <= 0 || Lc < 0 || page_size <= 0 || num_pages < 0 ||
+      N > INT32_MAX || Lc > INT32_MAX || num_pages > INT32_MAX || page_size > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (N == 0 || H == 0) return MTP_OK;
+  if (!q_nodes || !out || !k_tree || !v_tree || !tree_mask ||
+      (Lc > 0 && (!k_pages || !v_pages || !page_table)))
+    return MTP_ERR_NULL;
+  if (Lc > 0 && num_pages == 0) return MTP_ERR_SHAPE;
+  AttnArgs a{};
+  a.q = q_nodes;
+  a.q_sn = H * D;
+  a.q_sh = D;
+  a.kp = k_pages;
+  a.vp = v_pages;
+  a.table = page_table;
+  a.ld_tab = Lc;
+  a.Lc = (int)Lc;
+  a.page_size = (int)page_size;
+  a.npages = (int)num_pages;
+  a.p_sh = page_size * D;
+  a.p_sb = H * a.p_sh;
+  a.p_sp = a.p_sb;  // one batch row of pages
+  a.kd = k_tree;
+  a.vd = v_tree;
+  a.Lt = (int)N;
+  a.d_sh = D;
+  a.d_st = H * D;
+  a.mask = tree_mask;
+  a.mask_dt = mask_dtype;
+  a.mask_2d = 1;
+  a.out = out;
+  a.o_sn = H * D;
+  a.o_sh = D;
+  a.B = 1;
+  a.NQ = (int)N;
+  a.H = (int)H;
+  a.scale = scale;
+  return launch_attention(a, dtype, D, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

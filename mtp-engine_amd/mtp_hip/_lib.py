@@ -53,6 +53,14 @@ SIGNATURES = {
         _i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i64, _vp, _vp, _vp, _vp,
              _vp, _sz, _vp]),
     "mtp_verify_workspace_bytes": (_sz, [_i, _i64, _i64, _i64, _i64]),
+    "mtp_fused_paged_attention": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _f, _vp, _vp, _sz, _vp]),
+    "mtp_fused_tree_attention": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i, _f, _vp, _vp, _sz, _vp]),
+    "mtp_tree_verify_attention": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i, _f,
+             _vp, _vp, _sz, _vp]),
+    "mtp_attention_workspace_bytes": (_sz, [_i, _i64, _i64, _i64, _i64, _i64, _i64]),
 }
 
 _lib = None

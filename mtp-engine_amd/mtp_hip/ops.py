@@ -8,6 +8,7 @@ synchronising. Inputs must live on a HIP device.
 """
 from __future__ import annotations
 
+import math
 from typing import Optional, Tuple
 
 import torch
@@ -190,3 +191,109 @@ def multi_verify(hidden: torch.Tensor, weight: torch.Tensor, draft: torch.Tensor
     if return_top:
         return accept, accepted_n, corrected, top
     return accept, accepted_n, corrected
+
+
+def _mask_arg(mask: torch.Tensor) -> torch.Tensor:
+    mask = mask.contiguous()
+    if mask.dtype == torch.bool:
+        mask = mask.to(torch.uint8)
+    if mask.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.uint8):
+        mask = mask.to(torch.float32)
+    return mask
+
+
+def _attn_call(fn_name: str, q: torch.Tensor, B: int, NQ: int, H: int, D: int, Lc: int, Lt: int,
+               *args) -> None:
+    lib = _lib.load()
+    nbytes = lib.mtp_attention_workspace_bytes(code(q.dtype), B, NQ, H, D, Lc, Lt)
+    ws = _lib.workspace(q.device, nbytes)
+    st = getattr(lib, fn_name)(*args, ptr(ws), nbytes, _lib.stream_handle(q.device))
+    check(st, fn_name[4:])
+
+
+def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                    page_table: torch.Tensor, page_size: int, scale: Optional[float] = None):
+    """out[b, h] = softmax_t(q . k_t * scale) @ v_t over the paged keys of b."""
+    q = q.contiguous()
+    k_pages = k_pages.contiguous()
+    v_pages = v_pages.contiguous()
+    page_table = page_table.contiguous().to(torch.int32)
+    assert q.dim() == 3, "fused_paged_attention: q [B, H, D]"
+    B, H, D = q.shape
+    L = page_table.shape[-1]
+    assert k_pages.dim() == 5 and tuple(k_pages.shape[1:3]) == (B, H) and \
+        k_pages.shape[3] == page_size and k_pages.shape[4] == D, \
+        f"fused_paged_attention: pages must be [P, {B}, {H}, {page_size}, {D}], got {tuple(k_pages.shape)}"
+    assert v_pages.shape == k_pages.shape, "fused_paged_attention: k_pages / v_pages differ"
+    assert page_table.dim() == 2 and page_table.shape[0] == B, \
+        f"fused_paged_attention: page_table must be [{B}, L]"
+    assert k_pages.dtype == q.dtype and v_pages.dtype == q.dtype, "fused_paged_attention: dtypes differ"
+    _on_device("q", q, k_pages=k_pages, v_pages=v_pages, page_table=page_table)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty_like(q)
+    _attn_call("mtp_fused_paged_attention", q, B, 1, H, D, L, 0,
+               ptr(q), code(q.dtype), B, H, D, ptr(k_pages), ptr(v_pages), k_pages.shape[0],
+               ptr(page_table), L, int(page_size), float(scale), ptr(out))
+    return out
+
+
+def tree_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor,
+                   scale: Optional[float] = None):
+    """out[b, h] = softmax_l(q . k_l * scale where mask[l] > 0.5 else -inf) @ v_l."""
+    q = q.contiguous()
+    k = k.contiguous()
+    v = v.contiguous()
+    mask = _mask_arg(mask)
+    assert q.dim() == 3 and k.dim() == 4, "fused_tree_attention: q [B, H, D], k / v [B, H, L, D]"
+    B, H, D = q.shape
+    L = k.shape[2]
+    assert tuple(k.shape) == (B, H, L, D) and v.shape == k.shape, \
+        f"fused_tree_attention: k / v must be [{B}, {H}, L, {D}], got {tuple(k.shape)}"
+    assert mask.numel() == L, f"fused_tree_attention: mask has {mask.numel()} != {L}"
+    assert k.dtype == q.dtype and v.dtype == q.dtype, "fused_tree_attention: dtypes differ"
+    _on_device("q", q, k=k, v=v, mask=mask)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty_like(q)
+    _attn_call("mtp_fused_tree_attention", q, B, 1, H, D, 0, L,
+               ptr(q), code(q.dtype), B, H, D, ptr(k), ptr(v), L, ptr(mask), code(mask.dtype),
+               float(scale), ptr(out))
+    return out
+
+
+def tree_verify_attention(q_nodes: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                          page_table: torch.Tensor, page_size: int, k_tree: torch.Tensor,
+                          v_tree: torch.Tensor, tree_mask: torch.Tensor,
+                          scale: Optional[float] = None):
+    """Every tree node's query over the paged context plus its masked tree
+    nodes, under one softmax: out [N, H, D]."""
+    q_nodes = q_nodes.contiguous()
+    k_tree = k_tree.contiguous()
+    v_tree = v_tree.contiguous()
+    k_pages = k_pages.contiguous()
+    v_pages = v_pages.contiguous()
+    page_table = page_table.contiguous().to(torch.int32)
+    tree_mask = _mask_arg(tree_mask)
+    assert q_nodes.dim() == 3, "tree_verify_attention: q_nodes [N, H, D]"
+    N, H, D = q_nodes.shape
+    Lc = page_table.shape[-1]
+    assert tuple(k_tree.shape) == (N, H, D) and v_tree.shape == k_tree.shape, \
+        "tree_verify_attention: k_tree / v_tree must be [N, H, D]"
+    assert tuple(tree_mask.shape) == (N, N), "tree_verify_attention: tree_mask must be [N, N]"
+    assert k_pages.dim() == 5 and k_pages.shape[1] == 1 and k_pages.shape[2] == H and \
+        k_pages.shape[3] == page_size and k_pages.shape[4] == D and v_pages.shape == k_pages.shape, \
+        "tree_verify_attention: pages must be [P, 1, H, page_size, D]"
+    assert page_table.numel() == Lc, "tree_verify_attention: page_table [1, Lc]"
+    for t in (k_tree, v_tree, k_pages, v_pages):
+        assert t.dtype == q_nodes.dtype, "tree_verify_attention: dtypes differ"
+    _on_device("q_nodes", q_nodes, k_tree=k_tree, v_tree=v_tree, k_pages=k_pages,
+               v_pages=v_pages, page_table=page_table, tree_mask=tree_mask)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty_like(q_nodes)
+    _attn_call("mtp_tree_verify_attention", q_nodes, 1, N, H, D, Lc, N,
+               ptr(q_nodes), code(q_nodes.dtype), N, H, D, ptr(k_pages), ptr(v_pages),
+               k_pages.shape[0], ptr(page_table), Lc, int(page_size), ptr(k_tree), ptr(v_tree),
+               ptr(tree_mask), code(tree_mask.dtype), float(scale), ptr(out))
+    return out

@@ -148,3 +148,54 @@ def int4_linear(seed: int = 4, M: int = 256, K: int = 8192, N: int = 28672, grou
 # Algorithmic work per launch (bytes moved at least once, flops of the GEMM)
 def linear_bytes(M, N, K, x_bytes, w_bytes_per_elem, y_bytes, extra=0):
     return int(M * K * x_bytes + N * K * w_bytes_per_elem + M * N * y_bytes + extra)
+
+
+# --------------------------------------------------------------------------- #
+def draft_tree_mask(depth: int, max_branches: int) -> torch.Tensor:
+    """Ancestor-or-self mask [n, n] float32 of the breadth-first draft tree
+    with depth * max_branches nodes (SpeculativeDraftTree,
+    mtp_engine.py:651-680): row n is 1 on n and on every ancestor of n."""
+    n = depth * max_branches
+    parent = [-1] * n
+    frontier, idx = [0], 1
+    for _ in range(1, depth):
+        nxt = []
+        for p in frontier:
+            for _ in range(max_branches):
+                if idx < n:
+                    parent[idx] = p
+                    nxt.append(idx)
+                    idx += 1
+        frontier = nxt
+    mask = torch.zeros(n, n)
+    for i in range(n):
+        mask[i, i] = 1.0
+        p = parent[i]
+        while p >= 0:
+            mask[i, p] = 1.0
+            p = parent[p]
+    return mask
+
+
+def tree_verify(seed: int = 3, depth: int = 16, branches: int = 4, H: int = 32, D: int = 128,
+                Lc: int = 2048, page_size: int = 16, pages: int = 160, hidden: int = 4096,
+                N_out: int = 4096) -> Dict:
+    """Workload 4. Draws: q, k_tree, v_tree [N, H, D]; k_pages, v_pages
+    [pages, 1, H, page_size, D]; a permutation of the physical pages (the
+    first Lc / page_size of it hold the context, in order); W [N_out,
+    hidden] ~ 0.02 N(0, 1). All bf16 except the int32 table and the fp32
+    tree mask."""
+    g = _gen(seed)
+    mask = draft_tree_mask(depth, branches)
+    N = mask.shape[0]
+    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    k_tree = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    v_tree = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    k_pages = torch.randn(pages, 1, H, page_size, D, generator=g).to(torch.bfloat16)
+    v_pages = torch.randn(pages, 1, H, page_size, D, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(pages, generator=g)[: Lc // page_size]
+    table = perm.repeat_interleave(page_size).to(torch.int32)[None, :]
+    W = (0.02 * torch.randn(N_out, hidden, generator=g)).to(torch.bfloat16)
+    return dict(q=q, k_tree=k_tree, v_tree=v_tree, k_pages=k_pages, v_pages=v_pages,
+                page_table=table, page_size=page_size, tree_mask=mask, weight=W, eps=1e-6,
+                seed=seed)

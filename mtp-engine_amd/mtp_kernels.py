@@ -92,6 +92,51 @@ def fused_int4_matmul(
                            eps=eps)
 
 
+def fused_paged_attention(
+    q: torch.Tensor,
+    k_pages: torch.Tensor,
+    v_pages: torch.Tensor,
+    page_table: torch.Tensor,
+    page_size: int,
+    scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Single-query attention over a paged KV cache (mtp_kernels.py:1136-1162):
+    q [B, H, D]; pages [P, B, H, page_size, D]; page_table [B, L]; scale
+    defaults to 1/sqrt(D). Returns [B, H, D] in q's dtype."""
+    return ops.paged_attention(q, k_pages, v_pages, page_table, page_size, scale)
+
+
+def fused_tree_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    mask: torch.Tensor,
+    scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Single-query attention with a 1-D key mask (mtp_kernels.py:1165-1191):
+    q [B, H, D]; k / v [B, H, L, D]; mask [L] (> 0.5 attends)."""
+    return ops.tree_attention(q, k, v, mask, scale)
+
+
+def tree_verify_attention(
+    q_nodes: torch.Tensor,
+    k_pages: torch.Tensor,
+    v_pages: torch.Tensor,
+    page_table: torch.Tensor,
+    page_size: int,
+    k_tree: torch.Tensor,
+    v_tree: torch.Tensor,
+    tree_mask: torch.Tensor,
+    scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Extension: the tree-verify attention step in one launch — every
+    tree node's query over the paged context and its ancestors (tree_mask
+    [N, N] from SpeculativeDraftTree), one softmax per node. The reference
+    composes the same result from one fused_tree_attention call per node."""
+    return ops.tree_verify_attention(q_nodes, k_pages, v_pages, page_table, page_size, k_tree,
+                                     v_tree, tree_mask, scale)
+
+
 def pack_scales(weight_scales: List[torch.Tensor],
                 kv_scales: Optional[List[torch.Tensor]] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """One flat fp32 buffer holding every scale tensor back to back, plus the

@@ -309,3 +309,86 @@ def draft_tree(depth: int, max_branches: int = 8, mode: str = "tree") -> Tuple[t
         mask[n, n] = 1.0
     mask[0, 0] = 1.0
     return parent, mask
+
+
+# --------------------------------------------------------------------------- #
+# Attention (tree / paged) and the composed tree-verify step
+# --------------------------------------------------------------------------- #
+def _softmax_attend(qf, kf, vf, scale, valid=None):
+    """Single-query softmax attention in fp32 as the reference's eager twins
+    compute it (mtp_kernels.py:849-855, 865-871): scores = q.k * scale,
+    masked scores = -inf, m = amax, p = exp(s - m), out = (p / sum p) @ v.
+    qf [..., D], kf / vf [..., L, D], valid [..., L] bool or None."""
+    scores = torch.einsum("...d,...ld->...l", qf, kf) * scale
+    if valid is not None:
+        scores = torch.where(valid, scores, torch.full_like(scores, float("-inf")))
+    m = torch.amax(scores, dim=-1, keepdim=True)
+    p = torch.exp(scores - m)
+    l = p.sum(dim=-1, keepdim=True)
+    return torch.einsum("...l,...ld->...d", p / l, vf)
+
+
+def paged_attention(q, k_pages, v_pages, page_table, page_size: int, scale=None):
+    """_eager_paged_attention (mtp_kernels.py:832-856) with the wrapper's
+    defaults (1136-1149): q [B, H, D]; pages [P, B, H, page_size, D]; key t of
+    (b, h) is pages[page_table[b, t], b, h, t % page_size]; no mask; output in
+    q's dtype."""
+    q, k_pages, v_pages, page_table = map(_cpu, (q, k_pages, v_pages, page_table))
+    B, H, D = q.shape
+    L = page_table.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    page = page_table.long()
+    slot = torch.arange(L) % page_size
+    bi = torch.arange(B)[:, None]
+    kg = k_pages[page, bi, :, slot[None, :]]   # [B, L, H, D]
+    vg = v_pages[page, bi, :, slot[None, :]]
+    kf = kg.permute(0, 2, 1, 3).float()
+    vf = vg.permute(0, 2, 1, 3).float()
+    return _softmax_attend(q.float(), kf, vf, scale).to(q.dtype)
+
+
+def tree_attention(q, k, v, mask, scale=None):
+    """_eager_tree_attention (mtp_kernels.py:859-872) with the wrapper's
+    defaults (1165-1178): q [B, H, D]; k / v [B, H, L, D]; mask [L], key l is
+    attended where mask[l] > 0.5 (a fully masked row is NaN, as there)."""
+    q, k, v, mask = map(_cpu, (q, k, v, mask))
+    B, H, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    valid = (mask > 0.5)[None, None, :].expand(B, H, -1)
+    return _softmax_attend(q.float(), k.float(), v.float(), scale, valid).to(q.dtype)
+
+
+def tree_verify_attention(q_nodes, k_pages, v_pages, page_table, page_size: int, k_tree, v_tree,
+                          tree_mask, scale=None):
+    """The tree-verify attention step of the 64-node workload, as the
+    reference composes it from single-query calls: node n's query attends,
+    under one softmax, to the Lc context tokens of the paged cache (batch 0)
+    and to the tree nodes m with tree_mask[n, m] > 0.5 — i.e. one
+    _eager_tree_attention call per node (mtp_kernels.py:859-872) over
+    keys = context ++ tree with mask = ones(Lc) ++ tree_mask[n]
+    (tree mask from SpeculativeDraftTree, mtp_engine.py:671-680).
+    q_nodes / k_tree / v_tree [N, H, D]; pages [P, 1, H, page_size, D];
+    page_table [1, Lc] -> out [N, H, D] in q's dtype."""
+    q_nodes, k_pages, v_pages, page_table, k_tree, v_tree, tree_mask = map(
+        _cpu, (q_nodes, k_pages, v_pages, page_table, k_tree, v_tree, tree_mask))
+    N, H, D = q_nodes.shape
+    Lc = page_table.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    page = page_table[0].long()
+    slot = torch.arange(Lc) % page_size
+    kc = k_pages[page, 0, :, slot]                      # [Lc, H, D]
+    vc = v_pages[page, 0, :, slot]
+    keys = torch.cat([kc, k_tree], 0).permute(1, 0, 2).float()   # [H, Lc + N, D]
+    vals = torch.cat([vc, v_tree], 0).permute(1, 0, 2).float()
+    valid = torch.cat([torch.ones(N, Lc, dtype=torch.bool), tree_mask > 0.5], 1)  # [N, Lc + N]
+    qf = q_nodes.float().permute(1, 0, 2)               # [H, N, D]
+    scores = torch.einsum("hnd,hld->hnl", qf, keys) * scale
+    scores = torch.where(valid[None], scores, torch.full_like(scores, float("-inf")))
+    m = torch.amax(scores, dim=-1, keepdim=True)
+    p = torch.exp(scores - m)
+    l = p.sum(dim=-1, keepdim=True)
+    out = torch.einsum("hnl,hld->hnd", p / l, vals)
+    return out.permute(1, 0, 2).to(q_nodes.dtype)

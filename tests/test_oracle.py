@@ -281,3 +281,97 @@ def test_engine_rollback_known_answer():
     a_n, rej, toks, adv = O.engine_rollback(torch.ones(2, 4, dtype=torch.int8),
                                             torch.tensor([4, 4]), corr, draft)
     assert (a_n, rej, adv) == (4, False, 4) and torch.equal(toks, draft)
+
+
+# --------------------------------------------------------------------------- #
+# Attention pins
+# --------------------------------------------------------------------------- #
+def _attn_brute(q, k, v, valid, scale):
+    """float64 loops: softmax over valid keys of q.k*scale, then sum p*v."""
+    q, k, v = q.double(), k.double(), v.double()
+    L = k.shape[0]
+    s = [float((q * k[l]).sum()) * scale for l in range(L)]
+    idx = [l for l in range(L) if valid[l]]
+    m = max(s[l] for l in idx)
+    w = {l: math.exp(s[l] - m) for l in idx}
+    z = sum(w.values())
+    return sum((w[l] / z) * v[l] for l in idx)
+
+
+def test_tree_attention_brute_force():
+    g = torch.Generator().manual_seed(5)
+    B, H, L, D = 2, 3, 11, 8
+    q, k, v = (torch.randn(B, H, D, generator=g), torch.randn(B, H, L, D, generator=g),
+               torch.randn(B, H, L, D, generator=g))
+    mask = (torch.rand(L, generator=g) > 0.4).float()
+    mask[3] = 1.0
+    out = O.tree_attention(q, k, v, mask)
+    for b in range(B):
+        for h in range(H):
+            ref = _attn_brute(q[b, h], k[b, h], v[b, h], [bool(x > 0.5) for x in mask], 1 / math.sqrt(D))
+            assert torch.allclose(out[b, h].double(), ref, atol=1e-5)
+
+
+def test_tree_attention_all_ones_is_softmax_attention_and_masked_row_is_nan():
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(1, 2, 16, generator=g), torch.randn(1, 2, 9, 16, generator=g),
+               torch.randn(1, 2, 9, 16, generator=g))
+    out = O.tree_attention(q, k, v, torch.ones(9))
+    p = torch.softmax(torch.einsum("bhd,bhld->bhl", q.double(), k.double()) / 4.0, -1)
+    ref = torch.einsum("bhl,bhld->bhd", p, v.double())
+    assert torch.allclose(out.double(), ref, atol=1e-6)
+    assert torch.isnan(O.tree_attention(q, k, v, torch.zeros(9))).all()
+
+
+def _pages_from_contiguous(k, ps, perm):
+    """Pages [P, B, H, ps, D] holding contiguous k [B, H, L, D] with logical page j
+    stored at physical page perm[j]; table[b, t] = perm[t // ps]."""
+    B, H, L, D = k.shape
+    P = len(perm)
+    pages = torch.zeros(P, B, H, ps, D, dtype=k.dtype)
+    for j in range(L // ps):
+        pages[perm[j]] = k[:, :, j * ps:(j + 1) * ps].clone()
+    table = torch.tensor([[perm[t // ps] for t in range(L)] for _ in range(B)], dtype=torch.int32)
+    return pages, table
+
+
+def test_paged_attention_equals_contiguous_under_any_page_placement():
+    g = torch.Generator().manual_seed(7)
+    B, H, L, D, ps = 2, 3, 24, 16, 4
+    q = torch.randn(B, H, D, generator=g)
+    k = torch.randn(B, H, L, D, generator=g)
+    v = torch.randn(B, H, L, D, generator=g)
+    ref = O.tree_attention(q, k, v, torch.ones(L))
+    for perm in (list(range(L // ps)), [5, 0, 3, 1, 4, 2]):
+        kp, table = _pages_from_contiguous(k, ps, perm)
+        vp, _ = _pages_from_contiguous(v, ps, perm)
+        assert torch.allclose(O.paged_attention(q, kp, vp, table, ps), ref, atol=1e-6)
+
+
+def test_tree_verify_equals_per_node_single_query_calls():
+    g = torch.Generator().manual_seed(8)
+    N, H, D, Lc, ps = 5, 2, 16, 12, 4
+    _, tm = O.draft_tree(3, 2)
+    tm = tm[:N, :N]
+    qn = torch.randn(N, H, D, generator=g)
+    kc = torch.randn(1, H, Lc, D, generator=g)
+    vc = torch.randn(1, H, Lc, D, generator=g)
+    kt = torch.randn(N, H, D, generator=g)
+    vt = torch.randn(N, H, D, generator=g)
+    kp, table = _pages_from_contiguous(kc, ps, [2, 0, 1])
+    vp, _ = _pages_from_contiguous(vc, ps, [2, 0, 1])
+    out = O.tree_verify_attention(qn, kp, vp, table, ps, kt, vt, tm)
+    for n in range(N):
+        keys = torch.cat([kc, kt.permute(1, 0, 2)[None]], 2)
+        vals = torch.cat([vc, vt.permute(1, 0, 2)[None]], 2)
+        mask = torch.cat([torch.ones(Lc), tm[n]])
+        ref = O.tree_attention(qn[n][None], keys, vals, mask)[0]
+        assert torch.allclose(out[n], ref, atol=1e-6)
+
+
+def test_verify_tree_mask_pairs():
+    """The 64-node tree (depth 16, 4 branches): 1 + 4 + 16 + 43 nodes and
+    229 (node, ancestor-or-self) pairs."""
+    parent, mask = O.draft_tree(16, 4)
+    assert int((parent >= 0).sum()) + 1 == 64
+    assert int(mask.sum()) == 229
