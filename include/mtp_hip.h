@@ -239,6 +239,60 @@ int mtp_tree_verify_attention(const void *q_nodes, int dtype, int64_t N,
                               void *workspace, size_t workspace_bytes,
                               void *stream);
 
+/* ------------------------------------------------------------------------- */
+/* Quantizers                                                                */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Replaces quantize_fp8_e4m3(x) -> (x_fp8, scale) (mtp_kernels.py:704-713):
+ *   scale = amax(|x|) / 448 if amax > 0 else 1   (amax keeps NaN, NaN > 0 is false)
+ *   x_fp8 = e4m3fn(clamp(x / scale, -448, 448))  round to nearest even
+ * x: n elements in x_dtype; x_fp8: n bytes; scale: one fp32 (device).
+ * Needs mtp_quantize_workspace_bytes(n) of workspace.
+ */
+int mtp_quantize_fp8_e4m3(const void *x, int x_dtype, int64_t n, uint8_t *x_fp8,
+                          float *scale, void *workspace, size_t workspace_bytes,
+                          void *stream);
+size_t mtp_quantize_workspace_bytes(int64_t n);
+
+/*
+ * Per-output-channel fp8 weights: the scale rule of
+ * QuantScaleState.update_weight_scales (mtp_engine.py:617-622),
+ * wscale[n] = amax(|W[n, :]|) / 448 (0 -> 1), with each row quantized as
+ * quantize_fp8_e4m3 does: W_fp8[n, k] = e4m3fn(clamp(W[n, k] / wscale[n], +-448)).
+ * w [N, K] in w_dtype -> w_fp8 [N, K] bytes, wscale [N] fp32.
+ */
+int mtp_quantize_fp8_rows(const void *w, int w_dtype, int64_t N, int64_t K,
+                          uint8_t *w_fp8, float *wscale, void *stream);
+
+/*
+ * Replaces dequantize_fp8(x_fp8, scale) (mtp_kernels.py:726-727):
+ *   out = fp32(x_fp8) * scale, with one scale (per_row = 0) or one scale per
+ *   row of row_len elements (per_row = 1, the per-channel layout).
+ */
+int mtp_dequantize_fp8(const uint8_t *x_fp8, int64_t n, int64_t row_len,
+                       const float *scale, int per_row, float *out,
+                       void *stream);
+
+/*
+ * Replaces quantize_int4(x, group=32) -> (packed, scales)
+ * (mtp_kernels.py:730-751): per row and group of `group` columns,
+ *   s = amax / 7 if amax > 0 else 1,  q = clamp(round_half_even(w / s), -8, 7)
+ *   packed[n, k / 2] = (q[k] & 0xF) | (q[k + 1] & 0xF) << 4   (even k low)
+ * w [N, K] (K and group even) -> packed [N, K/2] u8, scales [N, ceil(K/group)] fp32.
+ */
+int mtp_quantize_int4(const void *w, int w_dtype, int64_t N, int64_t K,
+                      int64_t group, uint8_t *packed, float *scales,
+                      void *stream);
+
+/*
+ * Replaces dequantize_int4(packed, scales, K, group) (mtp_kernels.py:754-768):
+ *   out[n, k] = (nibble(n, k) - 8) * scales[n, k / group]   (fp32 [N, K])
+ */
+int mtp_dequantize_int4(const uint8_t *packed, const void *scales,
+                        int scale_dtype, int64_t N, int64_t K, int64_t group,
+                        float *out, void *stream);
+
 /* Workspace bytes for the attention entry points: B batch rows, NQ queries
  * per (batch, head) (1 for the two reference functions, N for tree verify),
  * Lc context keys, Lt dense keys (L of fused_tree_attention, N of tree

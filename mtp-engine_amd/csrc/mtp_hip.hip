@@ -10,6 +10,7 @@
 
 #include "attn_args.hpp"
 #include "generic.hpp"
+#include "quant.hpp"
 #include "ws_dispatch.hpp"
 
 using namespace mtp;
@@ -698,6 +699,86 @@ int mtp_tree_verify_attention(const void *q_nodes, int dtype, int64_t N, int64_t
   a.H = (int)H;
   a.scale = scale;
   return launch_attention(a, dtype, D, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+
+// ---------------------------------------------------------------------------
+// Quantizers
+size_t mtp_quantize_workspace_bytes(int64_t n) {
+  (void)n;
+  return kCounterBytes + 1024 * sizeof(float);
+}
+
+int mtp_quantize_fp8_e4m3(const void *x, int x_dtype, int64_t n, uint8_t *x_fp8, float *scale,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  if (!is_float_dt(x_dtype)) return MTP_ERR_DTYPE;
+  if (n <= 0) return MTP_ERR_SHAPE;  // torch's max of an empty tensor raises
+  if (!x || !x_fp8 || !scale) return MTP_ERR_NULL;
+  if (!workspace || workspace_bytes < mtp_quantize_workspace_bytes(n)) return MTP_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  unsigned char *w8 = (unsigned char *)workspace;
+  const unsigned blocks = (unsigned)std::min<int64_t>(1024, (n + 255) / 256);
+  hipLaunchKernelGGL(fp8_tensor_scale_kernel, dim3(blocks), dim3(256), 0, st, x, x_dtype, n,
+                     (float *)(w8 + kCounterBytes), (unsigned *)w8, scale);
+  int rc = launch_status();
+  if (rc != MTP_OK) return rc;
+  const unsigned qb = (unsigned)std::min<int64_t>(8192, ((n + 1) / 2 + 255) / 256);
+  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(qb), dim3(256), 0, st, x, x_dtype, n, n, scale, 0,
+                     x_fp8);
+  return launch_status();
+}
+
+int mtp_quantize_fp8_rows(const void *w, int w_dtype, int64_t N, int64_t K, uint8_t *w_fp8,
+                          float *wscale, void *stream) {
+  if (!is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
+  if (N < 0 || K <= 0 || N > INT32_MAX) return MTP_ERR_SHAPE;
+  if (N == 0) return MTP_OK;
+  if (!w || !w_fp8 || !wscale) return MTP_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(fp8_row_scale_kernel, dim3((unsigned)N), dim3(256), 0, st, w, w_dtype, K,
+                     wscale);
+  int rc = launch_status();
+  if (rc != MTP_OK) return rc;
+  const int64_t n = N * K;
+  const unsigned qb = (unsigned)std::min<int64_t>(8192, ((n + 1) / 2 + 255) / 256);
+  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(qb), dim3(256), 0, st, w, w_dtype, n, K, wscale, 1,
+                     w_fp8);
+  return launch_status();
+}
+
+int mtp_dequantize_fp8(const uint8_t *x_fp8, int64_t n, int64_t row_len, const float *scale,
+                       int per_row, float *out, void *stream) {
+  if (n < 0 || (per_row && row_len <= 0)) return MTP_ERR_SHAPE;
+  if (n == 0) return MTP_OK;
+  if (!x_fp8 || !scale || !out) return MTP_ERR_NULL;
+  const unsigned blocks = (unsigned)std::min<int64_t>(8192, (n + 255) / 256);
+  hipLaunchKernelGGL(fp8_dequantize_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     x_fp8, n, per_row ? row_len : 1, scale, per_row ? 1 : 0, out);
+  return launch_status();
+}
+
+int mtp_quantize_int4(const void *w, int w_dtype, int64_t N, int64_t K, int64_t group,
+                      uint8_t *packed, float *scales, void *stream) {
+  if (!is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
+  if (N < 0 || K <= 0 || (K & 1) || group <= 0 || (group & 1)) return MTP_ERR_SHAPE;
+  if (N == 0) return MTP_OK;
+  if (!w || !packed || !scales) return MTP_ERR_NULL;
+  const int64_t items = N * ((K + group - 1) / group);
+  hipLaunchKernelGGL(int4_quantize_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, w, w_dtype, N, K, group, packed, scales);
+  return launch_status();
+}
+
+int mtp_dequantize_int4(const uint8_t *packed, const void *scales, int scale_dtype, int64_t N,
+                        int64_t K, int64_t group, float *out, void *stream) {
+  if (!is_float_dt(scale_dtype)) return MTP_ERR_DTYPE;
+  if (N < 0 || K <= 0 || (K & 1) || group <= 0) return MTP_ERR_SHAPE;
+  if (N == 0) return MTP_OK;
+  if (!packed || !scales || !out) return MTP_ERR_NULL;
+  const unsigned blocks = (unsigned)std::min<int64_t>(8192, (N * K + 255) / 256);
+  hipLaunchKernelGGL(int4_dequantize_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     packed, scales, scale_dtype, N, K, group, out);
+  return launch_status();
 }
 
 }  // extern "C"

@@ -61,6 +61,12 @@ SIGNATURES = {
         _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i, _f,
              _vp, _vp, _sz, _vp]),
     "mtp_attention_workspace_bytes": (_sz, [_i, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "mtp_quantize_fp8_e4m3": (_i, [_vp, _i, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "mtp_quantize_workspace_bytes": (_sz, [_i64]),
+    "mtp_quantize_fp8_rows": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp]),
+    "mtp_dequantize_fp8": (_i, [_vp, _i64, _i64, _vp, _i, _vp, _vp]),
+    "mtp_quantize_int4": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "mtp_dequantize_int4": (_i, [_vp, _vp, _i, _i64, _i64, _i64, _vp, _vp]),
 }
 
 _lib = None

@@ -297,3 +297,88 @@ def tree_verify_attention(q_nodes: torch.Tensor, k_pages: torch.Tensor, v_pages:
                k_pages.shape[0], ptr(page_table), Lc, int(page_size), ptr(k_tree), ptr(v_tree),
                ptr(tree_mask), code(tree_mask.dtype), float(scale), ptr(out))
     return out
+
+
+def quantize_fp8_tensor(x: torch.Tensor):
+    """(x_fp8, scale): per-tensor amax / 448 scale and e4m3fn values."""
+    lib = _lib.load()
+    x = x.contiguous()
+    _on_device("x", x)
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    scale = torch.empty((), dtype=torch.float32, device=x.device)
+    n = x.numel()
+    assert n > 0, "quantize_fp8_e4m3: empty tensor"
+    nbytes = lib.mtp_quantize_workspace_bytes(n)
+    ws = _lib.workspace(x.device, nbytes)
+    st = lib.mtp_quantize_fp8_e4m3(ptr(x), code(x.dtype), n, ptr(q), ptr(scale), ptr(ws), nbytes,
+                                   _lib.stream_handle(x.device))
+    check(st, "quantize_fp8_e4m3")
+    return q, scale
+
+
+def quantize_fp8_rows(w: torch.Tensor):
+    """(w_fp8 [N, K], wscale [N]): per-row amax / 448 scales (0 -> 1)."""
+    lib = _lib.load()
+    w = w.contiguous()
+    assert w.dim() == 2, "quantize_fp8_rows: w [N, K]"
+    _on_device("w", w)
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=w.device)
+    s = torch.empty((N,), dtype=torch.float32, device=w.device)
+    st = lib.mtp_quantize_fp8_rows(ptr(w), code(w.dtype), N, K, ptr(q), ptr(s),
+                                   _lib.stream_handle(w.device))
+    check(st, "quantize_fp8_rows")
+    return q, s
+
+
+def dequantize_fp8(x_fp8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """fp32(x_fp8) * scale for a one-element scale or a per-row [rows, 1] scale."""
+    lib = _lib.load()
+    x_fp8 = x_fp8.contiguous()
+    scale = scale.contiguous().to(torch.float32)
+    _on_device("x_fp8", x_fp8, scale=scale)
+    out = torch.empty(x_fp8.shape, dtype=torch.float32, device=x_fp8.device)
+    if scale.numel() == 1:
+        per_row, row_len = 0, 1
+    else:
+        assert x_fp8.dim() >= 2 and scale.dim() == x_fp8.dim() and scale.shape[-1] == 1 and \
+            scale.numel() == x_fp8.numel() // x_fp8.shape[-1], \
+            "dequantize_fp8: scale must be one value or [rows, 1]"
+        per_row, row_len = 1, x_fp8.shape[-1]
+    st = lib.mtp_dequantize_fp8(ptr(x_fp8), x_fp8.numel(), row_len, ptr(scale), per_row, ptr(out),
+                                _lib.stream_handle(x_fp8.device))
+    check(st, "dequantize_fp8")
+    return out
+
+
+def quantize_int4(x: torch.Tensor, group: int = 32):
+    """(packed u8 [N, K/2], scales fp32 [N, ceil(K/group)])."""
+    lib = _lib.load()
+    x = x.contiguous()
+    assert x.dim() == 2, "quantize_int4: x [N, K]"
+    _on_device("x", x)
+    N, K = x.shape
+    ng = (K + group - 1) // group
+    packed = torch.empty((N, K // 2), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((N, ng), dtype=torch.float32, device=x.device)
+    st = lib.mtp_quantize_int4(ptr(x), code(x.dtype), N, K, int(group), ptr(packed), ptr(scales),
+                               _lib.stream_handle(x.device))
+    check(st, "quantize_int4")
+    return packed, scales
+
+
+def dequantize_int4(packed: torch.Tensor, scales: torch.Tensor, K: int, group: int) -> torch.Tensor:
+    """(nibble - 8) * scales[n, k // group] as fp32 [N, K]."""
+    lib = _lib.load()
+    packed = packed.contiguous()
+    scales = scales.contiguous()
+    _on_device("packed", packed, scales=scales)
+    N = packed.shape[0]
+    assert packed.dtype == torch.uint8 and packed.shape[1] == K // 2, \
+        f"dequantize_int4: packed must be uint8 [N, {K // 2}]"
+    assert tuple(scales.shape) == (N, (K + group - 1) // group), "dequantize_int4: scales shape"
+    out = torch.empty((N, K), dtype=torch.float32, device=packed.device)
+    st = lib.mtp_dequantize_int4(ptr(packed), ptr(scales), code(scales.dtype), N, K, int(group),
+                                 ptr(out), _lib.stream_handle(packed.device))
+    check(st, "dequantize_int4")
+    return out

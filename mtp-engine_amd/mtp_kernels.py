@@ -137,6 +137,34 @@ def tree_verify_attention(
                                      v_tree, tree_mask, scale)
 
 
+def quantize_fp8_e4m3(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(x_fp8, scale) with scale = amax(|x|) / 448 (1 when amax is not > 0)
+    (mtp_kernels.py:704-713)."""
+    return ops.quantize_fp8_tensor(x)
+
+
+def quantize_fp8_rows(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Extension: per-output-channel fp8 weights, the scale rule of
+    QuantScaleState.update_weight_scales (mtp_engine.py:617-622):
+    (w_fp8 [N, K], wscale [N])."""
+    return ops.quantize_fp8_rows(w)
+
+
+def dequantize_fp8(x_fp8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """fp32(x_fp8) * scale (mtp_kernels.py:726-727)."""
+    return ops.dequantize_fp8(x_fp8, scale)
+
+
+def quantize_int4(x: torch.Tensor, group: int = 32) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(packed uint8 [N, K/2], scales fp32 [N, ceil(K/group)]) (mtp_kernels.py:730-751)."""
+    return ops.quantize_int4(x, group)
+
+
+def dequantize_int4(packed: torch.Tensor, scales: torch.Tensor, K: int, group: int) -> torch.Tensor:
+    """(nibble - 8) * scale as fp32 [N, K] (mtp_kernels.py:754-768)."""
+    return ops.dequantize_int4(packed, scales, K, group)
+
+
 def pack_scales(weight_scales: List[torch.Tensor],
                 kv_scales: Optional[List[torch.Tensor]] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """One flat fp32 buffer holding every scale tensor back to back, plus the
