@@ -129,6 +129,41 @@ def make_fp32_case(torch, lib, L):
     return case
 
 
+def make_int4_case(torch, lib, L):
+    """INT4 weight-only RMSNorm+linear, x bf16 [256, 8192], W [28672, 8192]
+    group 128 with fp16 scales, gamma, bf16 out (one launch = the prologue
+    that writes the fp16 activations plus the MFMA GEMM)."""
+    from mtp_hip import workloads
+    d = workloads.int4_linear()
+    dev = torch.device("cuda")
+    M, K = d["x"].shape
+    N = d["packed"].shape[0]
+    group = d["group"]
+    wbytes = N * K // 2 + d["scales"].numel() * 2
+    nrot = rotations(wbytes)
+    pl = [d["packed"].to(dev) for _ in range(nrot)]
+    sl = [d["scales"].to(dev) for _ in range(nrot)]
+    x, gamma = d["x"].to(dev), d["gamma"].to(dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    nws = lib.mtp_rmsnorm_linear_workspace_bytes(L.BF16, L.U8, M, N, K)
+    ws = torch.zeros(max(nws, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.mtp_fused_int4_matmul
+    args = [(x.data_ptr(), L.BF16, M, K, p.data_ptr(), s.data_ptr(), L.F16, N, group,
+             L.NIBBLE_OFFSET8, gamma.data_ptr(), L.F32, ctypes.c_float(d["eps"]), 1,
+             y.data_ptr(), ws.data_ptr(), nws, stream) for p, s in zip(pl, sl)]
+
+    def launch(i):
+        st = fn(*args[i % nrot])
+        if st != 0:
+            raise RuntimeError(f"int4 launch failed: {st}")
+
+    nbytes = M * K * 2 + wbytes + K * 4 + M * N * 2
+    case = Case(f"int4_rmsnorm_linear_M{M}", launch, nbytes, 2 * M * N * K, "mfma", nrot)
+    case.keep = (pl, sl, x, gamma, y, ws)
+    return case
+
+
 def make_verify_case(torch, lib, L):
     import torch.nn.functional as F
     from mtp_hip import workloads
@@ -296,7 +331,8 @@ def main():
                      ("fp8_M32", lambda: make_fp8_case(torch, lib, L, 32)),
                      ("fp32_M16", lambda: make_fp32_case(torch, lib, L)),
                      ("multi_verify", lambda: make_verify_case(torch, lib, L)),
-                     ("tree_verify", lambda: make_tree_verify_case(torch, lib, L))]
+                     ("tree_verify", lambda: make_tree_verify_case(torch, lib, L)),
+                     ("int4_M256", lambda: make_int4_case(torch, lib, L))]
     if args.only:
         builders = [b for b in builders if b[0] in args.only.split(",")]
     for key, mk in builders:
@@ -327,6 +363,10 @@ def main():
         torch.cuda.synchronize()
         detail["copy_calib"] = dict(bytes_read=n, bytes_written=n, launches=5)
         del src, dst
+
+    if headline is None:  # --only without the headline workload: the detail alone
+        print(json.dumps({"detail": detail}), flush=True)
+        return
 
     cpu = None
     if not args.no_cpu:

@@ -121,9 +121,16 @@ int mtp_fused_rmsnorm_linear_fp8(const void *x, int x_dtype, int64_t M,
  *   y = cast_xdtype(xn @ Wdq^T),  Wdq[n, k] = nib(n, k) * scales[n, k / group]
  * nib(n, k) is nibble (k & 1) of packed[n, k / 2] (low nibble for even k),
  * decoded per `nibble` (MTP_NIBBLE_OFFSET8 = the reference). packed [N, K/2]
- * u8; scales [N, ceil(K/group)] in scale_dtype (F32 or F16).
- * norm = 0 is the reference (xn = x, no RMSNorm, G2); norm = 1 composes the
- * RMSNorm prologue xn = x * rstd * gamma (the INT4 RMSNorm+linear workload).
+ * u8; scales [N, ceil(K/group)] in scale_dtype (F32, F16 or BF16).
+ * norm = 0 is the reference (xn = x, or x * gamma when gamma is given; no
+ * RMSNorm, no bias); norm = 1 composes the RMSNorm prologue
+ * xn = x * rstd * gamma (the INT4 RMSNorm+linear workload).
+ * When K % 128 == 0, group % 32 == 0 and packed is 16-byte aligned, the
+ * MFMA path runs: it needs the workspace of
+ * mtp_rmsnorm_linear_workspace_bytes(x_dtype, MTP_U8, M, N, K) (fp16 copy
+ * of xn plus one float per row) and computes with weights decoded to fp16,
+ * so |scale| * 8 must stay below 65504 (scales under 2^-14 lose bits).
+ * Other shapes run a CUDA-core fallback without workspace.
  */
 int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K,
                           const uint8_t *packed, const void *scales,

@@ -1,0 +1,33 @@
+// Instantiations of the grouped INT4 GEMM (int4g.hpp).
+#include "int4g.hpp"
+
+namespace mtp {
+
+I4Kernel int4_gemm_pick(int mt, int na) {
+  if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1>;
+  if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1>;
+  if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2>;
+  return nullptr;
+}
+
+template <int XDT>
+I4PrepKernel int4_prep_x(int gdt) {
+  switch (gdt) {
+    case -1: return int4_prep_kernel<XDT, -1>;
+    case MTP_F32: return int4_prep_kernel<XDT, MTP_F32>;
+    case MTP_BF16: return int4_prep_kernel<XDT, MTP_BF16>;
+    case MTP_F16: return int4_prep_kernel<XDT, MTP_F16>;
+  }
+  return nullptr;
+}
+
+I4PrepKernel int4_prep(int xdt, int gdt) {
+  switch (xdt) {
+    case MTP_F32: return int4_prep_x<MTP_F32>(gdt);
+    case MTP_BF16: return int4_prep_x<MTP_BF16>(gdt);
+    case MTP_F16: return int4_prep_x<MTP_F16>(gdt);
+  }
+  return nullptr;
+}
+
+}  // namespace mtp

@@ -1,0 +1,473 @@
+// Grouped INT4 weight-only GEMM for gfx950 (the INT4 RMSNorm -> linear path):
+//   y[m, n] = omul[m] * sum_k xn[m, k] * ((nib(n, k) - 8) * scale[n, k / group])
+//
+// Two launches:
+//  1. int4_prep_kernel. One block per row of x (rows padded to whole tiles):
+//     xn = fp16(x * r * gamma * 2^-e * d(k)) with r = rstd (norm) or 1, 2^e
+//     the power of two that brings max_k |x * r * gamma| into [2^14, 2^15]
+//     (omul[m] = 2^e restores the row exactly; fp16 then keeps 11 bits for
+//     every entry down to 2^-25 of the row maximum; padded rows are zero),
+//     and d(k) = 1/16 for odd k, 1 for even k (the decode below yields 16
+//     times the weight at odd k, so the product is unchanged and exact).
+//     xn is written fragment-major (xfrag_piece): for each 32-row tile and
+//     unit of 128 k, eight 1 KB blocks, one per MFMA k-step, each laid out
+//     lane by lane as the B operand of v_mfma_f32_32x32x16_f16. A run of 8 k
+//     inside a lane's 16 bytes is permuted to (0, 4, 1, 5, 2, 6, 3, 7), the
+//     order in which the weight decode below produces k.
+//     The remaining blocks transpose the scales, [N, ng] in any float
+//     dtype, to fp16 [ng, ldst], so that the scales of the 32 weight rows a
+//     load instruction serves are 64 contiguous bytes.
+//  2. int4_gemm_kernel<MT, NA>: 4 waves; wave w owns 32 NA weight rows
+//     (NA 32-row A subtiles) against all 32 MT rows of x of the workgroup
+//     (MT 32-row B tiles); the workgroup covers 128 NA columns of y.
+//     K advances by units of 128 (64 bytes of a weight row). Per unit, the
+//     x tile (MT x 8 KB), the weight tile (128 NA rows x 64 bytes) and the
+//     fp16 scales of the rows are copied to LDS by buffer loads with the
+//     LDS bit (no register staging), into one of three LDS stages, two
+//     units ahead of the MFMAs; the copies are spread over the k-steps of
+//     the current unit. Each lane reads 32 bytes (64 nibbles) of each of
+//     its A rows from LDS and decodes them in registers, per dword w of 8
+//     nibbles n_0 .. n_7 (n_i at bit 4 i):
+//           v = w, then w >> 8:
+//             v & 0x000F000F | 0x64006400 -> fp16 pair (1024 + n_j, 1024 + n_j+4)
+//             v & 0x00F000F0 | 0x64006400 -> fp16 pair (1024 + 16 n_j+1, 1024 + 16 n_j+5)
+//           (pair - 1032) * s or (pair - 1152) * s -> (n - 8) or 16 (n - 8),
+//           exact, times s rounded once
+//         giving one fp16x8 A fragment per k-step of 16;
+//       - 8 k-steps of NA x MT v_mfma_f32_32x32x16_f16, fp32 accumulation.
+//     One barrier per unit: it publishes the unit's LDS stage and retires
+//     the stage that the next copy overwrites.
+//  The row groups of a column group sit on one XCD (workgroups b, b + 8,
+//  b + 16, ... are dispatched to the same XCD), so every read of a weight
+//  tile after the first tends to hit that XCD's L2.
+//  Limits: the decoded weights are fp16, so |scale| * 128 must stay below
+//  65504 and scales below 2^-14 lose precision (fp16 subnormals).
+#pragma once
+
+#include <type_traits>
+
+#include "int4g_args.hpp"
+#include "wstream.hpp"
+
+namespace mtp {
+
+typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+typedef __attribute__((ext_vector_type(8))) _Float16 h8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+// Slot of k-offset i inside an aligned run of 8: the decode yields k in the
+// slot order (0, 4, 1, 5, 2, 6, 3, 7).
+__device__ __forceinline__ int slot8(int i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
+
+// 16-byte piece of xn holding k = 8q .. 8q + 7 of row m (U units of 128 k):
+// tile m / 32, unit q / 16, k-step q % 8, lane 32 * ((q / 8) % 2) + m % 32.
+__device__ __forceinline__ int64_t xfrag_piece(int64_t m, int64_t q, int64_t U) {
+  const int64_t u = q >> 4, r = q & 15;
+  const int64_t lane = ((r >> 3) << 5) + (m & 31);
+  return ((((m >> 5) * U + u) * 8 + (r & 7)) << 6) + lane;
+}
+
+// Eight consecutive elements p[i .. i + 7] (i % 8 == 0, 16-byte aligned
+// rows) as fp32, with one or two vector loads.
+template <int DT>
+__device__ __forceinline__ void load8_f32(const void *p, int64_t i, float (&v)[8]) {
+  if constexpr (DT == MTP_F32) {
+    const float4 a = ((const float4 *)p)[i / 4], b = ((const float4 *)p)[i / 4 + 1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const u32x4 w = ((const u32x4 *)p)[i / 8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x2 t = unpack2<DT>(w[j]);
+      v[2 * j] = t[0];
+      v[2 * j + 1] = t[1];
+    }
+  }
+}
+
+// scales[n0 .. n0 + 63][0 .. ng) (dtype SDT) -> scT[g][n] fp16, n < N.
+// Eight loads are issued before their conversions and stores.
+template <int SDT>
+__device__ __forceinline__ void transpose_scales_t(const void *__restrict__ scales, int64_t N,
+                                                   int64_t ng, int64_t ldst, int64_t n0,
+                                                   uint16_t *__restrict__ scT) {
+  const int64_t total = 64 * ng;
+  for (int64_t i0 = threadIdx.x; i0 < total; i0 += 8 * 256) {
+    uint32_t raw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t i = i0 + 256 * j;
+      const int64_t n = n0 + (i & 63), g = i >> 6;
+      raw[j] = 0;
+      if (i < total && n < N) {
+        if constexpr (SDT == MTP_F32) raw[j] = ((const uint32_t *)scales)[n * ng + g];
+        else raw[j] = ((const uint16_t *)scales)[n * ng + g];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t i = i0 + 256 * j;
+      const int64_t n = n0 + (i & 63), g = i >> 6;
+      if (i < total && n < N) {
+        float f;
+        if constexpr (SDT == MTP_F32) f = __builtin_bit_cast(float, raw[j]);
+        else if constexpr (SDT == MTP_BF16) f = __builtin_bit_cast(float, raw[j] << 16);
+        else f = (float)__builtin_bit_cast(_Float16, (uint16_t)raw[j]);
+        scT[g * ldst + n] = __builtin_bit_cast(uint16_t, (_Float16)f);
+      }
+    }
+  }
+}
+__device__ __forceinline__ void transpose_scales(const void *scales, int sdt, int64_t N,
+                                                 int64_t ng, int64_t ldst, int64_t n0,
+                                                 uint16_t *scT) {
+  if (sdt == MTP_F32) transpose_scales_t<MTP_F32>(scales, N, ng, ldst, n0, scT);
+  else if (sdt == MTP_BF16) transpose_scales_t<MTP_BF16>(scales, N, ng, ldst, n0, scT);
+  else transpose_scales_t<MTP_F16>(scales, N, ng, ldst, n0, scT);
+}
+
+// Blocks [0, rows): row m of x -> xn (fp16, fragment-major), omul[m]; rows
+// m >= M are zero. Blocks [rows, rows + ceil(N / 64)): scales -> scT.
+// XDT: dtype of x; GDT: dtype of gamma, or -1 without gamma.
+template <int XDT, int GDT>
+__global__ void __launch_bounds__(256)
+int4_prep_kernel(const void *x, int64_t M, int64_t K, const void *gamma, float eps, int norm,
+                 void *xfv, float *omul, int64_t rows, const void *scales, int sdt, int64_t N,
+                 int64_t ng, int64_t ldst, uint16_t *scT) {
+  __shared__ float red[2][4];
+  u32x4 *xf = (u32x4 *)xfv;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) {
+    transpose_scales(scales, sdt, N, ng, ldst, (row - rows) * 64, scT);
+    return;
+  }
+  const int64_t U = K / 128, nq = K / 8;
+  if (row >= M) {
+    for (int64_t q = threadIdx.x; q < nq; q += 256)
+      xf[xfrag_piece(row, q, U)] = u32x4{0u, 0u, 0u, 0u};
+    if (threadIdx.x == 0) omul[row] = 0.f;
+    return;
+  }
+  const int64_t base = row * K;
+  float ss = 0.f, mx = 0.f;  // sum of x^2, max |x * gamma|
+#pragma unroll 4
+  for (int64_t q = threadIdx.x; q < nq; q += 256) {
+    float v[8], g[8];
+    load8_f32<XDT>(x, base + 8 * q, v);
+    if constexpr (GDT >= 0) load8_f32<GDT>(gamma, 8 * q, g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ss += v[i] * v[i];
+      mx = fmaxf(mx, fabsf(GDT >= 0 ? v[i] * g[i] : v[i]));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o, 64);
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = ss;
+    red[1][threadIdx.x >> 6] = mx;
+  }
+  __syncthreads();
+  ss = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+  mx = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  const float r = norm ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
+  const float top = mx * r;
+  int e = 0;
+  if (top > 0.f && top <= 3.0e38f) {
+    int ex;
+    frexpf(top, &ex);  // top <= 2^ex < 2 top
+    e = min(max(ex - 15, -100), 100);
+  }
+  const float mul = ldexpf(r, -e);
+  if (threadIdx.x == 0) omul[row] = ldexpf(1.0f, e);
+#pragma unroll 4
+  for (int64_t q = threadIdx.x; q < nq; q += 256) {
+    float v[8], g[8];
+    load8_f32<XDT>(x, base + 8 * q, v);
+    if constexpr (GDT >= 0) load8_f32<GDT>(gamma, 8 * q, g);
+    _Float16 hv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float t = v[i] * ((i & 1) ? mul * 0.0625f : mul);
+      if constexpr (GDT >= 0) t *= g[i];
+      hv[slot8(i)] = (_Float16)t;
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = (uint32_t)__builtin_bit_cast(uint16_t, hv[2 * j]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, hv[2 * j + 1]) << 16);
+    xf[xfrag_piece(row, q, U)] = o;
+  }
+}
+
+// 16 bytes per lane from a buffer straight into LDS (lane i writes bytes
+// 16 i .. 16 i + 15 after `lds`). The body exists only in the device pass:
+// the host pass cannot form the LDS address-space pointer, and an invalid
+// expression there would silently drop the host stubs of the kernels.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned char *lds,
+                                           uint32_t voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                           voff, soff, 0, 0);
+#endif
+}
+
+// f(integral_constant<int, I>) for I = LO .. HI - 1, each a compile-time
+// index (register arrays indexed by it stay in registers).
+template <int LO, int HI, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (LO < HI) {
+    f(std::integral_constant<int, LO>{});
+    static_for<LO + 1, HI>(f);
+  }
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding and
+// its LDS reads have returned, then meet the workgroup at a barrier. Unlike
+// __syncthreads() this does not drain every load: loads of later units stay
+// in flight. The memory clobber keeps the compiler from moving memory
+// accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int MT, int NA>
+__global__ void __launch_bounds__(256, 1)
+int4_gemm_kernel(const I4Args a) {
+  constexpr int BN = 128 * NA, UK = 128;
+  constexpr int TILE = 8 * 1024;          // bytes of one 32-row x tile per unit
+  constexpr int XST = MT * TILE;          // x bytes of one LDS stage
+  constexpr int WST = BN * 64;            // weight bytes of one LDS stage (64 per row)
+  constexpr int SST = 4 * 1024;           // scale bytes of one LDS stage (4 runs of 32 k)
+  constexpr int STAGE = XST + WST + SST;
+  constexpr int NS = 3;                   // LDS stages (copies run two units ahead)
+  constexpr int ND = 2 * MT;              // x copies per wave per unit
+  constexpr int NWL = BN / 64;            // weight copies per wave per unit (16 rows each)
+  constexpr int NV = NWL + 1 + ND;        // vector-memory instructions per wave per unit
+  __shared__ __attribute__((aligned(1024))) unsigned char xs[NS * STAGE];
+
+  const int th = threadIdx.x;
+  const int lane = th & 63;
+  const int wave = th >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+
+  // blockIdx -> (column group, row group): the row groups of column group
+  // c are workgroups with b % 8 == c % 8 (one XCD).
+  int cg, rg;
+  {
+    const int b = blockIdx.x;
+    const int sb = b >> 3;
+    const int q = sb / a.gm;
+    cg = q * 8 + (b & 7);
+    rg = sb - q * a.gm;
+  }
+  if (cg >= a.gn) return;
+  const int n0 = cg * BN;
+  const int nunits = a.K / UK;
+
+  // Weights: per unit the workgroup's BN rows x 64 bytes are copied to LDS
+  // row-major, 16 rows x 64 bytes per copy (copy c = wave + 4 i; lane L
+  // takes bytes 16 (L % 4) .. + 15 of row 16 c + L / 4). The MFMA A operand
+  // of subtile t is read back per lane: row wcol[t], bytes 32 h .. + 31.
+  const uint32_t ldw = (uint32_t)a.K / 2;
+  const int nrows = min(BN, a.N - n0);
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(a.packed + (int64_t)n0 * ldw, (uint32_t)nrows * ldw);
+  uint32_t wvo[NWL];
+#pragma unroll
+  for (int i = 0; i < NWL; ++i)
+    wvo[i] = (uint32_t)(16 * (wave + 4 * i) + (lane >> 2)) * ldw + 16u * (lane & 3);
+  int wcol[NA];  // row of the lane inside the workgroup's BN
+#pragma unroll
+  for (int t = 0; t < NA; ++t) wcol[t] = 32 * (NA * wave + t) + l32;
+  // fp16 scales, transposed: scale of row n, group g at scT[g * ldst + n].
+  // Per unit, wave w copies the scales of k-run w (k = 128 u + 32 w .. + 31)
+  // for the BN rows: lanes 0 .. BN / 8 - 1 copy 16 bytes each, the others
+  // read past the descriptor into an unused part of the LDS row.
+  const __amdgpu_buffer_rsrc_t srs =
+      make_rsrc((const uint16_t *)a.scales + n0, (uint32_t)(a.ng * a.ldst - n0) * 2u);
+  const uint32_t svo = lane < BN / 8 ? (uint32_t)lane * 16u : kOOB;
+  const uint32_t ldst2 = (uint32_t)a.ldst * 2u;
+  // x tiles of this workgroup: MT consecutive 32-row tiles of the
+  // fragment-major copy; tile T, unit u starts at byte (T * U + u) * TILE.
+  const unsigned char *xbase = (const unsigned char *)a.xn + (int64_t)rg * MT * nunits * TILE;
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(xbase, (uint32_t)(MT * nunits) * TILE);
+  // x copy c of a unit (c = wave + 4 i): tile c / 8, k-step c % 8; the
+  // unit goes in the scalar offset, the per-lane part is fixed.
+  uint32_t xvo[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
+    const int c = wave + 4 * i;
+    xvo[i] = (uint32_t)((c >> 3) * nunits * TILE + (c & 7) * 1024 + lane * 16);
+  }
+
+  // Vector-memory instruction v (0 <= v < NV) of unit `unit` into LDS
+  // stage `slot`: weight copies first, then the scale copy, then x copies.
+  auto issue = [&](auto vc, int unit, int slot) {
+    constexpr int v = decltype(vc)::value;
+    if constexpr (v < NWL) {
+      lds_copy16(wrs, xs + slot * STAGE + XST + (wave + 4 * v) * 1024, wvo[v], unit * 64);
+    } else if constexpr (v == NWL) {
+      const int k = unit * UK + 32 * wave;
+      const int g = a.glog >= 0 ? k >> a.glog : k / a.group;
+      lds_copy16(srs, xs + slot * STAGE + XST + WST + wave * 1024, svo, (int)((uint32_t)g * ldst2));
+    } else {
+      const int i = v - NWL - 1;
+      const int c = wave + 4 * i;
+      lds_copy16(xrs, xs + slot * STAGE + (c >> 3) * TILE + (c & 7) * 1024, xvo[i],
+                 unit * TILE);
+    }
+  };
+
+  f32x16 acc[NA][MT];
+#pragma unroll
+  for (int t = 0; t < NA; ++t)
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[t][j][e] = 0.f;
+
+  const uint32_t flip = a.nibble == MTP_NIBBLE_TWOS ? 0x88888888u : 0u;
+  const h2 m1032 = h2{(_Float16)(-1032.0f), (_Float16)(-1032.0f)};
+  const h2 m1152 = h2{(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
+  // One unit: 8 k-steps, software-pipelined one step deep (the LDS reads
+  // and the weight decode of step s + 1 are issued before the MFMAs of s).
+  // The NV vector-memory instructions of unit `nunit` (two units ahead) are
+  // spread over the k-steps so that the memory pipeline's queues never fill
+  // and block the in-order issue of the MFMAs behind them.
+  auto compute = [&](int slot, int nunit, int nslot) {
+    const unsigned char *sx = xs + slot * STAGE + lane * 16;
+    const unsigned char *sw = xs + slot * STAGE + XST;
+    const unsigned char *ss = xs + slot * STAGE + XST + WST;
+    u32x4 wr[NA][2];
+#pragma unroll
+    for (int t = 0; t < NA; ++t)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) wr[t][e] = *(const u32x4 *)(sw + wcol[t] * 64 + 32 * h + 16 * e);
+    h2 s2[NA][2];
+#pragma unroll
+    for (int t = 0; t < NA; ++t)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const _Float16 f = *(const _Float16 *)(ss + (2 * h + g) * 1024 + wcol[t] * 2);
+        s2[t][g] = h2{f, f};
+      }
+    auto decode = [&](h8 (&af)[NA], int s) {
+#pragma unroll
+      for (int t = 0; t < NA; ++t) {
+        const uint32_t w = wr[t][s >> 2][s & 3] ^ flip;
+        const uint32_t w8 = w >> 8;
+        const h2 sv = s2[t][s >> 2];
+        const uint32_t q0 = (w & 0x000F000Fu) | 0x64006400u;
+        const uint32_t q1 = (w & 0x00F000F0u) | 0x64006400u;
+        const uint32_t q2 = (w8 & 0x000F000Fu) | 0x64006400u;
+        const uint32_t q3 = (w8 & 0x00F000F0u) | 0x64006400u;
+        u32x4 o;
+        o[0] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, q0) + m1032) * sv);
+        o[1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, q1) + m1152) * sv);
+        o[2] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, q2) + m1032) * sv);
+        o[3] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, q3) + m1152) * sv);
+        af[t] = __builtin_bit_cast(h8, o);
+      }
+    };
+    auto read_b = [&](h8 (&bv)[MT], int s) {
+#pragma unroll
+      for (int j = 0; j < MT; ++j) bv[j] = *(const h8 *)(sx + j * TILE + s * 1024);
+    };
+    h8 af[2][NA], bv[2][MT];
+    read_b(bv[0], 0);
+    decode(af[0], 0);
+    static_for<0, 8>([&](auto sc_) {
+      constexpr int s = decltype(sc_)::value;
+      static_for<s * NV / 8, (s + 1) * NV / 8>([&](auto vc) { issue(vc, nunit, nslot); });
+      if constexpr (s + 1 < 8) {
+        read_b(bv[(s + 1) & 1], s + 1);
+        decode(af[(s + 1) & 1], s + 1);
+      }
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int t = 0; t < NA; ++t)
+          acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s & 1][t], bv[s & 1][j],
+                                                             acc[t][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // Pipeline: units u + 1 and u + 2 are in flight while unit u computes.
+  // The loop is unrolled by the ring length so that stage r's offsets are
+  // compile-time constants. Copies are issued for every u + 2, also past
+  // the last unit: such a copy reads zeros (past the end of its
+  // descriptor) or bytes of another tile or row, into a stage that is
+  // never computed on, so the count of instructions behind the copies of
+  // unit u is always NV.
+  static_for<0, NV>([&](auto vc) { issue(vc, 0, 0); });
+  __builtin_amdgcn_sched_barrier(0);  // every copy of unit 0 before any of unit 1
+  static_for<0, NV>([&](auto vc) { issue(vc, 1, 1); });
+  auto step = [&](auto rc, int u) {
+    constexpr int r = decltype(rc)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's copies of unit u have landed once at most the NV
+    // instructions of unit u + 1 are outstanding; the barrier makes every
+    // wave's copies visible and retires the stage of unit u - 1, which the
+    // copies of unit u + 2 overwrite
+    wait_vmcnt_barrier<NV>();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(r, u + 2, (r + 2) % 3);
+  };
+  int u = 0;
+  for (; u + 3 <= nunits; u += 3) {
+    step(std::integral_constant<int, 0>{}, u);
+    step(std::integral_constant<int, 1>{}, u + 1);
+    step(std::integral_constant<int, 2>{}, u + 2);
+  }
+  if (u < nunits) step(std::integral_constant<int, 0>{}, u);
+  if (u + 1 < nunits) step(std::integral_constant<int, 1>{}, u + 1);
+  // no copy into LDS may still be in flight when the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // epilogue: acc[t][j][e] = y[m][n] with m = m0 + 32 j + l32 and
+  // n = n0 + wcol[t] - l32 + 8 (e / 4) + 4 h + e % 4.
+  const int m0 = rg * MT * 32;
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const int m = m0 + 32 * j + l32;
+    if (m >= a.M) continue;
+    const float om = a.omul[m];
+#pragma unroll
+    for (int t = 0; t < NA; ++t) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wcol[t] - l32 + 8 * g + 4 * h;
+        const int64_t base = (int64_t)m * a.N + n;
+        const float v0 = acc[t][j][4 * g] * om, v1 = acc[t][j][4 * g + 1] * om;
+        const float v2 = acc[t][j][4 * g + 2] * om, v3 = acc[t][j][4 * g + 3] * om;
+        if (n + 3 < a.N && a.yvec) {
+          uint2 pk;
+          if (a.ydt == MTP_BF16) {
+            pk.x = pack2<MTP_BF16>(v0, v1);
+            pk.y = pack2<MTP_BF16>(v2, v3);
+          } else {
+            pk.x = pack2<MTP_F16>(v0, v1);
+            pk.y = pack2<MTP_F16>(v2, v3);
+          }
+          *(uint2 *)((uint16_t *)a.y + base) = pk;
+        } else {
+          const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < a.N) store_from_f32(a.y, a.ydt, base + e, v[e]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace mtp

@@ -1,0 +1,34 @@
+// Arguments and instantiation accessors of the grouped INT4 GEMM (int4g.hpp),
+// shared by its instantiation unit and the host planner.
+#pragma once
+
+#include <stdint.h>
+
+namespace mtp {
+
+struct I4Args {
+  const void *xn;         // fp16 x, fragment-major, rows padded to gm * MT * 32
+  const float *omul;      // [M] output multiplier of each row
+  const uint8_t *packed;  // [N, K / 2]
+  const void *scales;     // fp16 [ng, ldst], transposed by the prep kernel
+  int ldst;               // row stride of the transposed scales (>= columns of y covered)
+  void *y;                // [M, N] in ydt
+  int ydt;
+  int yvec;               // N % 4 == 0 and y 8-byte aligned (16-bit ydt)
+  int M, N, K, group, ng;
+  int glog;               // log2(group) when group is a power of two, else -1
+  int nibble;             // MTP_NIBBLE_OFFSET8 / MTP_NIBBLE_TWOS
+  int gn, gm;             // column groups of 128 NA and row groups of 32 MT
+};
+
+typedef void (*I4Kernel)(I4Args);
+typedef void (*I4PrepKernel)(const void *, int64_t, int64_t, const void *, float, int, void *,
+                             float *, int64_t, const void *, int, int64_t, int64_t, int64_t,
+                             uint16_t *);
+// GEMM kernel for MT 32-row x tiles and 128 NA weight rows per workgroup
+// ((1, 1), (2, 1) or (4, 2)), or null.
+I4Kernel int4_gemm_pick(int mt, int na);
+// Prep kernel for x dtype xdt and gamma dtype gdt (-1: no gamma), or null.
+I4PrepKernel int4_prep(int xdt, int gdt);
+
+}  // namespace mtp

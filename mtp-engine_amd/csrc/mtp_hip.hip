@@ -10,6 +10,7 @@
 
 #include "attn_args.hpp"
 #include "generic.hpp"
+#include "int4g_args.hpp"
 #include "quant.hpp"
 #include "ws_dispatch.hpp"
 
@@ -427,6 +428,88 @@ int launch_attention(AttnArgs &a, int ct, int64_t D, void *ws, size_t ws_bytes, 
 
 bool mask_dt_ok(int dt) { return is_float_dt(dt) || dt == MTP_U8; }
 
+// ---------------------------------------------------------------------------
+// INT4 MFMA path: x -> (fragment-major fp16 copy, omul) in the workspace,
+// then the decode-in-register GEMM. Workspace: the fp16 copy (rows padded
+// to whole row groups) at 0, omul after it.
+struct Int4Tiles {
+  int mt, na;   // 32-row x tiles and 128-row weight groups per workgroup
+  int64_t gm;   // row groups
+  int64_t rows; // padded rows
+};
+Int4Tiles int4_tiles(int64_t M) {
+  Int4Tiles t;
+  t.mt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
+  t.na = t.mt == 4 ? 2 : 1;
+  t.gm = (M + 32 * t.mt - 1) / (32 * t.mt);
+  t.rows = t.gm * 32 * t.mt;
+  return t;
+}
+// Row stride of the transposed fp16 scales: the columns the GEMM covers.
+int64_t int4_ldst(int64_t M, int64_t N) {
+  const int64_t bn = 128 * int4_tiles(M).na;
+  return (N + bn - 1) / bn * bn;
+}
+size_t int4_xn_bytes(int64_t M, int64_t K) {
+  return align_up((size_t)int4_tiles(M).rows * K * 2, 256);
+}
+size_t int4_omul_bytes(int64_t M) { return align_up((size_t)int4_tiles(M).rows * 4, 256); }
+size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t ng) {
+  return int4_xn_bytes(M, K) + int4_omul_bytes(M) +
+         align_up((size_t)ng * int4_ldst(M, N) * 2, 256);
+}
+constexpr int64_t kInt4MaxK = (int64_t)1 << 23;  // keeps every buffer offset in 32 bits
+bool int4_fast(int64_t M, int64_t N, int64_t K, int64_t group) {
+  if (K <= 0 || K % 128 != 0 || K > kInt4MaxK || group % 32 != 0) return false;
+  const int64_t ng = (K + group - 1) / group;
+  return ng * int4_ldst(M, N) * 2 < ((int64_t)1 << 31);
+}
+
+int launch_int4(const void *x, int xdt, int64_t M, int64_t K, const uint8_t *packed,
+                const void *scales, int sdt, int64_t N, int64_t group, int nibble,
+                const void *gamma, int gdt, float eps, int norm, void *y, void *ws,
+                size_t ws_bytes, hipStream_t st) {
+  const int64_t ng = (K + group - 1) / group;
+  if (!ws || ws_bytes < int4_ws_bytes(M, N, K, ng)) return MTP_ERR_WORKSPACE;
+  if (((uintptr_t)ws & 15u) != 0) return MTP_ERR_ALIGN;
+  const Int4Tiles tl = int4_tiles(M);
+  I4Kernel gemm = int4_gemm_pick(tl.mt, tl.na);
+  if (!gemm) return MTP_ERR_DTYPE;
+  const int64_t gn = (N + 128 * tl.na - 1) / (128 * tl.na);
+  const int64_t blocks = (gn + 7) / 8 * 8 * tl.gm;
+  const int64_t sblocks = (N + 63) / 64;  // scale-transpose blocks of the prep launch
+  if (blocks > INT32_MAX || tl.rows + sblocks > INT32_MAX) return MTP_ERR_SHAPE;
+  unsigned char *w8 = (unsigned char *)ws;
+  I4Args a;
+  a.xn = w8;
+  a.omul = (const float *)(w8 + int4_xn_bytes(M, K));
+  uint16_t *scT = (uint16_t *)(w8 + int4_xn_bytes(M, K) + int4_omul_bytes(M));
+  a.ldst = (int)int4_ldst(M, N);
+  I4PrepKernel prep = int4_prep(xdt, gamma ? gdt : -1);
+  if (!prep) return MTP_ERR_DTYPE;
+  hipLaunchKernelGGL(prep, dim3((unsigned)(tl.rows + sblocks)), dim3(256), 0, st, x, M, K, gamma,
+                     eps, norm, (void *)a.xn, (float *)a.omul, tl.rows, scales, sdt, N, ng,
+                     (int64_t)a.ldst, scT);
+  int s = launch_status();
+  if (s != MTP_OK) return s;
+  a.packed = packed;
+  a.scales = scT;
+  a.y = y;
+  a.ydt = xdt;
+  a.yvec = xdt != MTP_F32 && N % 4 == 0 && ((uintptr_t)y & 7u) == 0;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.group = (int)group;
+  a.ng = (int)ng;
+  a.glog = (group & (group - 1)) == 0 ? __builtin_ctzll((unsigned long long)group) : -1;
+  a.nibble = nibble;
+  a.gn = (int)gn;
+  a.gm = (int)tl.gm;
+  hipLaunchKernelGGL(gemm, dim3((unsigned)blocks), dim3(256), 0, st, a);
+  return launch_status();
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -452,7 +535,8 @@ const char *mtp_last_hip_error(void) { return g_last_hip_error; }
 
 size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, int64_t N,
                                           int64_t K) {
-  if (w_kind == MTP_U8) return 0;  // packed INT4: no split-K workspace yet
+  // packed INT4: enough for every group the MFMA path takes (group >= 32)
+  if (w_kind == MTP_U8) return int4_fast(M, N, K, 32) ? int4_ws_bytes(M, N, K, K / 32) : 0;
   // enough for the call with or without gamma
   size_t most = 0;
   for (int gam = 0; gam < 2; ++gam) {
@@ -487,8 +571,6 @@ int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K, cons
                           const void *scales, int scale_dtype, int64_t N, int64_t group,
                           int nibble, const void *gamma, int gamma_dtype, float eps, int norm,
                           void *y, void *workspace, size_t workspace_bytes, void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (!is_float_dt(x_dtype)) return MTP_ERR_DTYPE;
   if (scale_dtype != MTP_F32 && scale_dtype != MTP_F16 && scale_dtype != MTP_BF16)
     return MTP_ERR_DTYPE;
@@ -499,6 +581,10 @@ int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K, cons
     return MTP_ERR_SHAPE;
   if (M == 0 || N == 0) return MTP_OK;
   if (!y || (K > 0 && (!x || !packed || !scales))) return MTP_ERR_NULL;
+  if (int4_fast(M, N, K, group) && aligned16(packed) && aligned16(x) &&
+      (!gamma || aligned16(gamma)))
+    return launch_int4(x, x_dtype, M, K, packed, scales, scale_dtype, N, group, nibble, gamma,
+                       gamma_dtype, eps, norm, y, workspace, workspace_bytes, (hipStream_t)stream);
   return launch_generic_linear(x, x_dtype, packed, MTP_U8, nullptr, scales, scale_dtype,
                                (int)group, nibble, gamma, gamma_dtype, nullptr, 0, y, M, N, K,
                                eps, 1.0f, norm, (hipStream_t)stream);
