@@ -12,6 +12,7 @@
 #include "generic.hpp"
 #include "int4g_args.hpp"
 #include "quant.hpp"
+#include "sk_args.hpp"
 #include "ws_dispatch.hpp"
 
 using namespace mtp;
@@ -302,6 +303,97 @@ int launch_wsp(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Skinny weight-streaming plan (sk.hpp): at most 64 rows of 16-bit x, W of
+// fp8 or the same 16-bit type, whole 128-byte stages per W row.
+struct PlanSk {
+  bool ok = false;
+  int ct = 0, wt = 0, mt = 0;
+  bool gam = false;
+  int G = 0, S = 1, kb_per = 0, nkb = 0;
+  size_t xf_off = 0, part_off = 0, total = 0;
+};
+
+constexpr int kSkMinBlocks = 200;  // aim for most of the 256 CUs busy
+constexpr int kSkMinStages = 4;    // stages per split at least
+
+// Tile: 64 columns x all rows of x (<= 64); K-splits only while the grid is
+// short of CUs. Workspace: counters, the xn blocks, split-K partials.
+PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
+  PlanSk p;
+  p.ct = ct;
+  p.wt = wt;
+  p.gam = gam;
+  if (ct != MTP_BF16 && ct != MTP_F16) return p;
+  if (wt != MTP_FP8E4M3 && wt != ct) return p;
+  // 33 .. 64 rows: the row-chunk kernel (wsp) is faster below that
+  const char *force = std::getenv("MTP_SK_SPLITS");
+  const bool forced = force && *force;
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0 || (M <= 32 && !forced)) return p;
+  if (std::getenv("MTP_WS_TUNE") && *std::getenv("MTP_WS_TUNE")) return p;  // sweeps of wsp
+  const int wb = dtype_bytes(wt);
+  if ((K * wb) % kSkUB != 0 || K > 256 * 8 * kSkPrepChunks) return p;
+  // buffer descriptors: the workgroup's W rows, all xn blocks
+  if ((int64_t)kSkBN * K * wb >= (int64_t)1 << 31 || (int64_t)sk_xf_bytes(M, K) >= (int64_t)1 << 31)
+    return p;
+  p.mt = M <= 32 ? 1 : 2;
+  p.G = (int)((N + kSkBN - 1) / kSkBN);
+  p.nkb = (int)(K * wb / kSkUB);
+  int S = 1;
+  if (forced) {
+    S = std::max(1, std::atoi(force));
+  } else {
+    while ((int64_t)p.G * S < kSkMinBlocks && p.nkb / (S + 1) >= kSkMinStages) ++S;
+  }
+  if (S > p.nkb) S = p.nkb;
+  p.kb_per = (p.nkb + S - 1) / S;
+  p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  if ((int64_t)p.G * p.S > INT32_MAX) return p;
+  if (p.S > 1 && p.G > kCounterSlots) return p;
+  size_t off = kCounterBytes;
+  p.xf_off = off;
+  off += align_up(sk_xf_bytes(M, K), 256);
+  if (p.S > 1) {
+    const size_t part = (size_t)p.S * p.G * sk_tile_bytes(p.mt);
+    if (part >= ((size_t)1 << 31)) return p;
+    p.part_off = off;
+    off += align_up(part, 256);
+  }
+  p.total = off;
+  p.ok = sk_pick(ct, wt, p.mt) != nullptr && sk_prep_pick(ct, wt, gam) != nullptr;
+  return p;
+}
+
+int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int norm,
+              SkArgs &a, void *ws, hipStream_t st) {
+  SkKernel k = sk_pick(p.ct, p.wt, p.mt);
+  SkPrepKernel pk = sk_prep_pick(p.ct, p.wt, p.gam);
+  if (!k || !pk) return MTP_ERR_DTYPE;
+  unsigned char *w8 = (unsigned char *)ws;
+  SkPrepArgs pa;
+  pa.x = x;
+  pa.gamma = gamma;
+  pa.xf = w8 + p.xf_off;
+  pa.M = a.M;
+  pa.K = a.K;
+  pa.norm = norm;
+  pa.eps = eps;
+  hipLaunchKernelGGL(pk, dim3((unsigned)(32 * p.mt)), dim3(256), 0, st, pa);
+  int s = launch_status();
+  if (s != MTP_OK) return s;
+  a.xf = pa.xf;
+  a.G = p.G;
+  a.S = p.S;
+  a.kb_per = p.kb_per;
+  a.nkb = p.nkb;
+  if (p.S > 1) {
+    a.part = (float *)(w8 + p.part_off);
+    a.ticket = (unsigned *)w8;
+  }
+  hipLaunchKernelGGL(k, dim3((unsigned)(p.G * p.S)), dim3(256), 0, st, a);
+  return launch_status();
+}
+
 int launch_generic_linear(const void *x, int xt, const void *w, int wt, const float *wscale,
                           const void *i4scale, int i4dt, int group, int nib, const void *gamma,
                           int gt, const void *bias, int bt, void *y, int64_t M, int64_t N,
@@ -329,14 +421,7 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   if (!x && K > 0) return MTP_ERR_NULL;
   if ((!w && K > 0) || !y) return MTP_ERR_NULL;
   hipStream_t st = (hipStream_t)stream;
-  PlanX p = make_plan_x(xt, wt, M, N, K, gamma != nullptr);
   const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!gamma || aligned16(gamma));
-  // the tiled kernel reads gamma as fp32 (the Python shim upcasts it)
-  if (!p.ok || !aligned || (gamma && gt != MTP_F32)) {
-    return launch_generic_linear(x, xt, w, wt, wscale, nullptr, 0, 0, -1, gamma, gt, bias, bt, y,
-                                 M, N, K, eps, scale, norm, st);
-  }
-  if (p.total > 0 && (!ws || ws_bytes < p.total)) return MTP_ERR_WORKSPACE;
   WsArgs a{};
   a.x = x;
   a.w = w;
@@ -351,6 +436,28 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
+  const PlanSk ps = make_plan_sk(xt, wt, M, N, K, gamma != nullptr);
+  if (ps.ok && aligned && (!gamma || gt == MTP_F32)) {
+    if (!ws || ws_bytes < ps.total) return MTP_ERR_WORKSPACE;
+    SkArgs sa{};
+    sa.w = w;
+    sa.wscale = wscale;
+    sa.bias = bias;
+    sa.bias_dt = bt;
+    sa.y = y;
+    sa.M = (int)M;
+    sa.N = (int)N;
+    sa.K = (int)K;
+    sa.scale = scale;
+    return launch_sk(ps, x, (const float *)gamma, eps, norm, sa, ws, st);
+  }
+  PlanX p = make_plan_x(xt, wt, M, N, K, gamma != nullptr);
+  // the tiled kernel reads gamma as fp32 (the Python shim upcasts it)
+  if (!p.ok || !aligned || (gamma && gt != MTP_F32)) {
+    return launch_generic_linear(x, xt, w, wt, wscale, nullptr, 0, 0, -1, gamma, gt, bias, bt, y,
+                                 M, N, K, eps, scale, norm, st);
+  }
+  if (p.total > 0 && (!ws || ws_bytes < p.total)) return MTP_ERR_WORKSPACE;
   return launch_wsp(p, a, ws, st);
 }
 
@@ -542,6 +649,8 @@ size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, in
   for (int gam = 0; gam < 2; ++gam) {
     PlanX p = make_plan_x(x_dtype, w_kind, M, N, K, gam != 0);
     if (p.ok && p.total > most) most = p.total;
+    PlanSk q = make_plan_sk(x_dtype, w_kind, M, N, K, gam != 0);
+    if (q.ok && q.total > most) most = q.total;
   }
   return most;
 }

@@ -1,0 +1,426 @@
+// Skinny weight-streaming GEMM for gfx950: the RMSNorm -> linear path at
+// M <= 64 rows of x with 16-bit x (bf16 / f16) and fp8-e4m3 or 16-bit W.
+//
+//   y[m, n] = (xn[m, :] . W[n, :]) * wscale[n] + bias[n], times scale
+//   xn[m, k] = x[m, k] * rs[m] * gamma[k],  rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) (norm) or 1
+//
+// Two launches:
+//  1. sk_prep_kernel, one block per row of x (rows padded to whole 32-row
+//     tiles, padding rows zero): xn rounded to the MFMA input type (the type
+//     of x), written as the B operands of v_mfma_f32_32x32x16: for each
+//     32-row tile, stage and k-step, one 1 KB block of 64 lanes x 16 bytes.
+//     Doing this once per launch instead of once per column group keeps the
+//     GEMM free of per-element vector work on x.
+//  2. sk_kernel: bound by reading W once from HBM. A "stage" is 128 bytes
+//     of every W row (128 fp8 or 64 16-bit values of k). Workgroup = 4 waves
+//     and a tile of 64 output columns x all (<= 64) rows of x; the waves
+//     split the k-steps of each stage (fp8: wave w takes k-steps 2w, 2w + 1;
+//     16-bit W: k-step w), so every operand is read by exactly one wave, and
+//     their partial sums meet in LDS at the end. Per stage the workgroup
+//     copies W (64 rows x 128 bytes: one instruction covers 8 rows x 128
+//     contiguous bytes, the pattern that streams HBM fastest among the ones
+//     an MFMA row layout allows) into registers, and each wave loads its own
+//     xn blocks (1 KB contiguous per MFMA operand) into registers. W bytes in
+//     flight per CU set the bandwidth (register loads keep more of them in
+//     flight per CU than buffer loads into LDS), so both register rings run
+//     NS - 1 stages ahead (NS = 8: 56 KB of W per CU); the loads of a stage
+//     are spread over the wave's MFMAs. One stage before it is used, a stage
+//     of W goes from registers to LDS (double-buffered), where each wave
+//     reads the A operands of its k-steps. One barrier per stage.
+//     W sits in LDS row-major with 16-byte chunk c of row r at position
+//     c ^ (r % 8) (the A-operand reads of 32 consecutive rows then hit
+//     distinct banks); for fp8 the A operand is upcast exactly in registers.
+//     k-slot order: within 32 k of a stage (two k-steps for fp8), lane group
+//     g = lane / 32 holds k 16 g .. 16 g + 15, the first 8 in k-step 2p, the
+//     other 8 in k-step 2p + 1 (16-bit W: k-step j, lane group g holds
+//     k 16 j + 8 g .. + 7); the prep writes xn in the same order.
+//  End: S == 1 applies the epilogue directly; otherwise the workgroups of a
+//  tile hand fp32 partial sums to the last one to arrive (coherent stores,
+//  arrival ticket; see the hand-off notes in mtp_common.hpp), which sums them
+//  in split order.
+#pragma once
+
+#include <type_traits>
+
+#include "sk_args.hpp"
+#include "wstream.hpp"
+
+namespace mtp {
+
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+
+template <int CT>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (CT == MTP_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// (k-step, lane group) of 16-byte chunk q (8 k) of a stage.
+template <bool FP8>
+__device__ __forceinline__ void sk_chunk_slot(int q, int &j, int &g) {
+  if constexpr (FP8) {
+    j = 2 * (q >> 2) + (q & 1);
+    g = (q >> 1) & 1;
+  } else {
+    j = q >> 1;
+    g = q & 1;
+  }
+}
+
+// 16 bytes per lane from a buffer straight into LDS (lane i writes bytes
+// 16 i .. 16 i + 15 after `lds`). The body exists only in the device pass:
+// the host pass cannot form the LDS address-space pointer, and an invalid
+// expression there would silently drop the host stubs of the kernels.
+template <int AUX>
+__device__ __forceinline__ void sk_lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned char *lds,
+                                              uint32_t voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                           voff, soff, 0, AUX);
+#endif
+}
+
+// f(integral_constant<int, I>) for I = LO .. HI - 1.
+template <int LO, int HI, class F>
+__device__ __forceinline__ void sk_static_for(F &&f) {
+  if constexpr (LO < HI) {
+    f(std::integral_constant<int, LO>{});
+    sk_static_for<LO + 1, HI>(f);
+  }
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding and
+// its LDS reads have returned, then meet the workgroup at a barrier; loads
+// of later stages stay in flight. The memory clobber keeps the compiler from
+// moving memory accesses across it.
+template <int N>
+__device__ __forceinline__ void sk_wait_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// 1. prep: row m of x -> xn blocks
+template <int CT, bool FP8, bool GAM>
+__global__ void __launch_bounds__(256)
+sk_prep_kernel(const SkPrepArgs a) {
+  constexpr int UK = FP8 ? 128 : 64, KS = UK / 16, QPS = UK / 8;
+  __shared__ float red[4];
+  const int m = blockIdx.x, th = threadIdx.x;
+  const int K = a.K, nst = K / UK;
+  u32x4 *xf = (u32x4 *)a.xf;
+  // block (tile, stage, k-step) is 1 KB = 64 lanes of 16 bytes
+  auto out = [&](int q_all) -> u32x4 & {
+    const int st = q_all / QPS, q = q_all - st * QPS;
+    int j, g;
+    sk_chunk_slot<FP8>(q, j, g);
+    return xf[(((int64_t)(m >> 5) * nst + st) * KS + j) * 64 + 32 * g + (m & 31)];
+  };
+  const int nq = K / 8;
+  if (m >= a.M) {
+    for (int q = th; q < nq; q += 256) out(q) = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  // the row is read once: up to kSkPrepChunks 16-byte chunks per thread
+  // stay in registers between the sum of squares and the scaling
+  const u32x4 *xr = (const u32x4 *)((const uint16_t *)a.x + (int64_t)m * K);
+  u32x4 xv[kSkPrepChunks];
+#pragma unroll
+  for (int i = 0; i < kSkPrepChunks; ++i) {
+    const int q = th + 256 * i;
+    xv[i] = q < nq ? xr[q] : u32x4{0u, 0u, 0u, 0u};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSkPrepChunks; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f32x2 f = unpack2<CT>(xv[i][e]);
+      ss += f[0] * f[0] + f[1] * f[1];
+    }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if ((th & 63) == 0) red[th >> 6] = ss;
+  __syncthreads();
+  const float rs =
+      a.norm ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps) : 1.0f;
+#pragma unroll
+  for (int i = 0; i < kSkPrepChunks; ++i) {
+    const int q = th + 256 * i;
+    if (q >= nq) break;
+    const u32x4 v = xv[i];
+    f32x4 g0 = f32x4{1.f, 1.f, 1.f, 1.f}, g1 = g0;
+    if constexpr (GAM) {
+      g0 = ((const f32x4 *)a.gamma)[2 * q];
+      g1 = ((const f32x4 *)a.gamma)[2 * q + 1];
+    }
+    const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f32x2 f = unpack2<CT>(v[e]);
+      o[e] = pack2<CT>(f[0] * rs * g[2 * e], f[1] * rs * g[2 * e + 1]);
+    }
+    out(q) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. GEMM
+template <int CT, int WT, int MT>
+__global__ void __launch_bounds__(256, 1)
+sk_kernel(const SkArgs a) {
+  constexpr bool FP8 = WT == MTP_FP8E4M3;
+  constexpr int UK = FP8 ? 128 : 64;         // k per stage
+  constexpr int KS = UK / 16;                // MFMA k-steps per stage
+  constexpr int KPW = KS / 4;                // k-steps per wave per stage
+  constexpr int STAGE = kSkBN * kSkUB;       // W bytes of one LDS buffer (8 KB)
+  constexpr int NS = 8;                      // register ring stages (loads run NS - 1 ahead)
+  constexpr int NWC = STAGE / 1024 / 4;      // W loads per wave per stage (2)
+  constexpr int NXL = MT * KPW;              // xn loads per wave per stage
+  constexpr int NV = NWC + NXL;              // vector-memory instructions per wave per stage
+  constexpr int RED = 4 * 2 * MT * 64 * 64;  // end-phase partial tiles of the four waves
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * STAGE > RED ? 2 * STAGE : RED];
+  static_assert((NS - 1) * NV < 64, "vmcnt is 6 bits");
+  __shared__ int s_flag;
+
+  const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
+  const int N = a.N, K = a.K;
+
+  // blockIdx -> (column tile, split): the splits of a tile are consecutive
+  const int tile = (int)blockIdx.x / a.S, sp = (int)blockIdx.x - tile * a.S;
+  const int n0 = tile * kSkBN;
+  const int st0 = sp * a.kb_per;
+  const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // stages of this split (>= 1)
+
+  // W load c (c = wave + 4 i): rows 8 c .. 8 c + 7, lane l: row 8 c + l / 8;
+  // the LDS write of a load is 64 lanes x 16 bytes contiguous, so the
+  // swizzle (chunk c' of the row at position c' ^ (row % 8)) is in the chunk
+  // a lane fetches
+  const uint32_t ldw = (uint32_t)K * (FP8 ? 1u : 2u);
+  const int nrows = min(kSkBN, N - n0);
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc((const unsigned char *)a.w + (int64_t)n0 * ldw, (uint32_t)nrows * ldw);
+  uint32_t wvo[NWC];
+#pragma unroll
+  for (int i = 0; i < NWC; ++i) {
+    const int row = 8 * (wave + 4 * i) + (lane >> 3);
+    const int chunk = (lane & 7) ^ (row & 7);
+    wvo[i] = (uint32_t)row * ldw + (uint32_t)st0 * kSkUB + 16u * chunk;
+  }
+  // xn load i = t * KPW + jj of the wave: tile t, k-step wave * KPW + jj
+  const int nst_all = a.nkb;
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xf, (uint32_t)(MT * nst_all * KS) * 1024u);
+  uint32_t xvo[NXL];
+#pragma unroll
+  for (int i = 0; i < NXL; ++i) {
+    const int t = i / KPW, j = wave * KPW + i % KPW;
+    xvo[i] = (uint32_t)(((t * nst_all + st0) * KS + j) * 1024 + lane * 16);
+  }
+  u32x4 xr[NS][NXL];   // xn register ring
+  u32x4 wr[NS][NWC];   // W register ring
+
+  // Instruction v (0 <= v < NV) of stage st into ring slot `slot`. Stages
+  // past the split read zeros or other stages' bytes into a slot that is
+  // never computed on, so the count of instructions per stage is always NV.
+  auto issue = [&](auto vc, int st, auto slotc) {
+    constexpr int v = decltype(vc)::value, slot = decltype(slotc)::value;
+    if constexpr (v < NWC) {
+      wr[slot][v] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[v], st * kSkUB, 2));
+    } else {
+      constexpr int i = v - NWC;
+      xr[slot][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i], st * KS * 1024, 0));
+    }
+  };
+
+  f32x16 acc[2][MT];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[u][t][e] = 0.f;
+
+  // This wave's k-steps of a stage (A from W rows 32 u + lane % 32, B from
+  // the xn blocks), with the copies of stage `nst_` spread over them.
+  const int ag = lane >> 5;
+  // W of ring slot `slot` to LDS buffer b
+  auto w_to_lds = [&](auto slotc, int b) {
+    constexpr int slot = decltype(slotc)::value;
+#pragma unroll
+    for (int v = 0; v < NWC; ++v)
+      *(u32x4 *)(lds + b * STAGE + (wave + 4 * v) * 1024 + lane * 16) = wr[slot][v];
+  };
+  auto compute = [&](auto slotc, int nst_, auto nslotc) {
+    constexpr int slot = decltype(slotc)::value;
+    const unsigned char *base = lds + (slot & 1) * STAGE;
+    sk_static_for<0, KPW>([&](auto jc) {
+      constexpr int jj = decltype(jc)::value;
+      sk_static_for<jj * NV / KPW, (jj + 1) * NV / KPW>([&](auto vc) { issue(vc, nst_, nslotc); });
+      const int j = wave * KPW + jj;  // k-step of the stage
+      u32x4 av[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int row = 32 * u + (lane & 31);
+        if constexpr (FP8) {
+          // chunk 2 (j / 2) + g holds k-steps j (bytes 0..7) and j + 1 (8..15)
+          const int c = 2 * (j >> 1) + ag;
+          const u32x4 w = *(const u32x4 *)(base + row * kSkUB + ((c ^ (row & 7)) << 4));
+          const int h = (j & 1) * 2;
+          av[u][0] = fp8x2_to_ct<CT, false>(w[h]);
+          av[u][1] = fp8x2_to_ct<CT, true>(w[h]);
+          av[u][2] = fp8x2_to_ct<CT, false>(w[h + 1]);
+          av[u][3] = fp8x2_to_ct<CT, true>(w[h + 1]);
+        } else {
+          const int c = 2 * j + ag;
+          av[u] = *(const u32x4 *)(base + row * kSkUB + ((c ^ (row & 7)) << 4));
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const u32x4 bv = xr[slot][t * KPW + jj];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[u][t] = mfma32<CT>(av[u], bv, acc[u][t]);
+      }
+    });
+  };
+
+  // Pipeline: stages s + 1 .. s + NS - 1 are loading while s computes; the
+  // loop is unrolled by the ring length so the ring slots are compile-time
+  // registers (moving registers between slots would wait for the loads just
+  // issued). Scheduling barriers keep each phase in place: work on a slot
+  // hoisted ahead of its phase would wait for loads issued just before, and
+  // the prologue keeps the loop's load order (the wait counts at the loop
+  // head are the minimum over both ways in).
+  sk_static_for<0, NS - 1>([&](auto pc) {
+    sk_static_for<0, NV>([&](auto vc) { issue(vc, decltype(pc)::value, pc); });
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  w_to_lds(std::integral_constant<int, 0>{}, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  auto step = [&](auto rc, int s) {
+    constexpr int r = decltype(rc)::value;  // s % NS
+    __builtin_amdgcn_sched_barrier(0);
+    // W of stage s + 1 to the other LDS buffer (the barrier below publishes
+    // it; buffer s & 1 is rewritten only after the next barrier)
+    if (s + 1 < nst) w_to_lds(std::integral_constant<int, (r + 1) % NS>{}, (s + 1) & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // MFMAs of stage s; ring slot r - 1 (stage s - 1, done) refills with
+    // stage s + NS - 1
+    compute(rc, s + NS - 1, std::integral_constant<int, (r + NS - 1) % NS>{});
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  int s = 0;
+  for (; s + NS <= nst; s += NS)
+    sk_static_for<0, NS>([&](auto rc) { step(rc, s + decltype(rc)::value); });
+  sk_static_for<0, NS - 1>([&](auto rc) {
+    if (s + decltype(rc)::value < nst) step(rc, s + decltype(rc)::value);
+  });
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last stage
+  __syncthreads();
+
+  // ---- the four waves' partial tiles meet in LDS: wave w sums output tile
+  // (u, t) = (w % 2, w / 2) (waves past the MT tiles only contribute)
+  f32x16 *red = (f32x16 *)lds;  // [wave][u][t][lane]
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[((wave * 2 + u) * MT + t) * 64 + lane] = acc[u][t];
+  __syncthreads();
+  const int ou = wave & 1, ot = wave >> 1;
+  const bool owner = ot < MT;
+  f32x16 v;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) v[e] = 0.f;
+  if (owner) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v += red[((q * 2 + ou) * MT + ot) * 64 + lane];
+  }
+
+  // lane's outputs: v[e] = D[n][m], m = 32 ot + lane % 32,
+  // n = n0 + 32 ou + 8 (e / 4) + 4 (lane / 32) + e % 4
+  auto finish = [&](const f32x16 &r) {
+    const int m = 32 * ot + (lane & 31);
+    if (m >= a.M) return;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = n0 + 32 * ou + 8 * g + 4 * ag;
+      float o[4];
+#pragma unroll
+      for (int jx = 0; jx < 4; ++jx) {
+        const int nn = min(n + jx, N - 1);
+        float x = r[4 * g + jx];
+        if (a.wscale) x *= a.wscale[nn];
+        if (a.bias) x += load_as_f32(a.bias, a.bias_dt, nn);
+        o[jx] = x * a.scale;
+      }
+      const int64_t yb = (int64_t)m * N + n;
+      if (n + 3 < N && (N & 3) == 0) {
+        uint2 pk;
+        pk.x = pack2<CT>(o[0], o[1]);
+        pk.y = pack2<CT>(o[2], o[3]);
+        *(uint2 *)((uint16_t *)a.y + yb) = pk;
+      } else {
+        for (int jx = 0; jx < 4; ++jx)
+          if (n + jx < N) store_from_f32(a.y, CT, yb + jx, o[jx]);
+      }
+    }
+  };
+
+  if (a.S == 1) {
+    if (owner) finish(v);
+    return;
+  }
+
+  // Split-K hand-off: partial [tile][split][owner wave][4 quads][lane] of
+  // f32x4 (consecutive lanes write consecutive 16 bytes), coherent stores.
+  constexpr uint32_t TILEB = (uint32_t)2 * MT * 4u * 64u * 16u;
+  const uint32_t part_bytes = (uint32_t)(a.S * a.G) * TILEB;
+  const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, part_bytes);
+  auto part_off = [&](int q, int g4) {
+    return (uint32_t)(tile * a.S + q) * TILEB +
+           ((uint32_t)(wave * 4 + g4) * 64u + (uint32_t)lane) * 16u;
+  };
+  if (owner) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4 p4 = f32x4{v[4 * g4], v[4 * g4 + 1], v[4 * g4 + 2], v[4 * g4 + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, p4), prs,
+                                             part_off(sp, g4), 0, kSc1);
+    }
+  }
+  wait_stores();
+  __syncthreads();
+  if (th == 0) s_flag = (ticket_add(a.ticket + tile) == (unsigned)(a.S - 1));
+  __syncthreads();
+  if (!s_flag) return;
+  if (owner) {
+    f32x16 tot;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tot[e] = 0.f;
+    for (int q = 0; q < a.S; ++q) {
+      f32x4 pv[4];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        pv[g4] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, part_off(q, g4), 0, kSc1));
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tot[4 * g4 + e] += pv[g4][e];
+    }
+    finish(tot);
+  }
+  if (th == 0) ticket_reset(a.ticket + tile);
+}
+
+}  // namespace mtp

@@ -19,11 +19,12 @@ DEV = "cuda"
 
 @pytest.fixture(autouse=True)
 def _tune_reset():
-    old = os.environ.pop("MTP_WS_TUNE", None)
+    old = {k: os.environ.pop(k, None) for k in ("MTP_WS_TUNE", "MTP_SK_SPLITS")}
     yield
-    os.environ.pop("MTP_WS_TUNE", None)
-    if old is not None:
-        os.environ["MTP_WS_TUNE"] = old
+    for k, v in old.items():
+        os.environ.pop(k, None)
+        if v is not None:
+            os.environ[k] = v
 
 
 def _inputs(M, N, K, dtype, seed, bias=True, gamma=True):
@@ -143,6 +144,40 @@ def test_fp8_tile_variants_and_splits(tune, M, xdtype):
     ref = O.rmsnorm_linear_fp8(x, wq, ws, None, 1e-6, gamma=gm)
     ok, worst = close(y, ref, RTOL[xdtype])
     assert ok, f"worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("splits", ["1", "2", "3", "5"])
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (7, 300, 512), (33, 260, 1024), (64, 1000, 2048)])
+@pytest.mark.parametrize("wkind", ["fp8", "same"])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
+    """The skinny weight-streaming kernel (M <= 64, 16-bit x, fp8 or 16-bit
+    W): every forced K-split count, ragged M and N, with and without gamma
+    and norm, against the oracle."""
+    os.environ["MTP_SK_SPLITS"] = splits
+    from mtp_hip import ops
+    print(f"case splits={splits} M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
+    g = torch.Generator().manual_seed(M * 131 + N + K)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(xdtype)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+        y2 = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), None, 1e-6, norm=False)
+        ref2 = O.rmsnorm_linear_fp8(x, wq, ws, None, 1e-6, norm=False)
+    else:
+        Wc = W.to(xdtype)
+        y = ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5, gamma=gm)
+        y2 = ops.rmsnorm_linear(_dev(x), _dev(Wc), None, 1e-6, 1.0, norm=False)
+        ref2 = O.rmsnorm_linear(x, Wc, None, 1e-6, 1.0, norm=False)
+    torch.cuda.synchronize()
+    for out, r in ((y, ref), (y2, ref2)):
+        ok, worst = close(out, r, 2e-2)
+        assert ok, f"worst err/bound = {worst:.3g}"
 
 
 @pytest.mark.parametrize("M", [8, 32, 64])
