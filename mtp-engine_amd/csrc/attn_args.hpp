@@ -6,7 +6,11 @@
 
 namespace mtp {
 
-constexpr int kAttnMaxChunks = 32;  // context chunks per (b, h)
+constexpr int kAttnMaxChunks = 64;     // key chunks per (b, h)
+constexpr int kAttnBlock = 64;         // keys per block (two wave halves of 32)
+constexpr int kAttnRing = 2;           // key blocks in flight per workgroup
+constexpr int kAttnTableWindow = 1024; // context keys whose pages sit in LDS at once
+constexpr float kAttnRescale = 8.f;    // max gain (natural log) before O is rescaled
 
 struct AttnArgs {
   const void *q;               // element strides: batch, query, head (d stride 1)
@@ -25,16 +29,16 @@ struct AttnArgs {
   int64_t o_sb, o_sn, o_sh;
   int B, NQ, H;
   float scale;
-  int nchunks, chunk_blocks;   // context blocks of 32 keys per chunk
-  float *part;                 // [B*H][nchunks][16*QT][D]
-  float *ml;                   // [B*H][nchunks][16*QT][2]
-  unsigned *ticket;            // [B*H]
+  int nchunks, chunk_blocks;   // blocks of kAttnBlock keys (context, then dense) per chunk
+  float *part;                 // [B*H][nchunks][16*ceil(NQ/16)][D]
+  float *ml;                   // [B*H][nchunks][16*ceil(NQ/16)][2]
 };
 
 typedef void (*AttnKernel)(AttnArgs);
-// Defined in attn.hip: the MFMA kernel for (compute type, head dim, query
-// tiles of 16) or null, and the fallback kernel.
-AttnKernel attn_pick(int ct, int d, int qt);
+// Defined in attn.hip: the MFMA kernel and the chunk merge for (compute
+// type, head dim) or null, and the fallback kernel.
+AttnKernel attn_pick(int ct, int d);
+AttnKernel attn_merge_pick(int ct, int d);
 void (*attn_generic())(AttnArgs, int, int);
 
 }  // namespace mtp

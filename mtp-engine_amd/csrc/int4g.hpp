@@ -217,27 +217,6 @@ __device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned ch
 #endif
 }
 
-// f(integral_constant<int, I>) for I = LO .. HI - 1, each a compile-time
-// index (register arrays indexed by it stay in registers).
-template <int LO, int HI, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (LO < HI) {
-    f(std::integral_constant<int, LO>{});
-    static_for<LO + 1, HI>(f);
-  }
-}
-
-// Wait until at most N vector-memory loads of this wave are outstanding and
-// its LDS reads have returned, then meet the workgroup at a barrier. Unlike
-// __syncthreads() this does not drain every load: loads of later units stay
-// in flight. The memory clobber keeps the compiler from moving memory
-// accesses across it.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
 template <int MT, int NA>
 __global__ void __launch_bounds__(256, 1)
 int4_gemm_kernel(const I4Args a) {

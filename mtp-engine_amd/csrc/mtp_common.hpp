@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/mtp_hip.h"
 
 namespace mtp {
@@ -132,6 +134,54 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---- compile-time loops and split waits -------------------------------------
+// f(integral_constant<int, I>) for I = LO .. HI - 1, each a compile-time
+// index (register arrays indexed by it stay in registers).
+template <int LO, int HI, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (LO < HI) {
+    f(std::integral_constant<int, LO>{});
+    static_for<LO + 1, HI>(f);
+  }
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding and
+// its LDS accesses have completed, then meet the workgroup at a barrier.
+// Unlike __syncthreads() this does not drain every load: later loads stay in
+// flight. The memory clobber keeps the compiler from moving memory accesses
+// across it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+// LDS accesses completed, then the workgroup barrier; vector-memory loads
+// stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// ---- cross-lane reductions without LDS ----------------------------------------
+// v_permlane16_swap(x, x) gives lane l the pair (x[l], x[l ^ 16]) and
+// v_permlane32_swap(x, x) the pair (x[l], x[l ^ 32]) (in lane order), so
+// two of them reduce over the lanes l, l ^ 16, l ^ 32, l ^ 48 on the VALU.
+__device__ __forceinline__ float max_over_lane_groups(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float sum_over_lane_groups(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
 // ---- argmax ordering (torch.argmax) ---------------------------------------

@@ -464,7 +464,7 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
 
 // ---------------------------------------------------------------------------
 // Attention: plan and launch.
-constexpr int kAttnTargetBlocks = 256;  // one workgroup per CU
+constexpr int kAttnTargetBlocks = 256;  // 8-wave workgroups that fill the chip once
 
 struct AttnPlan {
   int qt = 0, nchunks = 1, chunk_blocks = 0;
@@ -472,21 +472,24 @@ struct AttnPlan {
   size_t part_off = 0, ml_off = 0, total = 0;
 };
 
+// Key blocks of kAttnBlock (context, then dense) are split into chunks of
+// chunk_blocks consecutive blocks, one workgroup each, so that the launch
+// has at most kAttnTargetBlocks workgroups (one per CU) where the heads
+// allow; MTP_ATTN_CHUNK_BLOCKS overrides the chunk length.
 AttnPlan make_attn_plan(int ct, int64_t B, int64_t NQ, int64_t H, int64_t D, int64_t Lc,
                         int64_t Lt) {
   AttnPlan p;
   p.fast = (ct == MTP_BF16 || ct == MTP_F16) && (D == 64 || D == 128) && NQ >= 1 && NQ <= 64;
-  const int64_t nctx_blocks = (Lc + 31) / 32;
   if (!p.fast) return p;  // the fallback needs no workspace
   p.qt = (int)((NQ + 15) / 16);
-  int nch = 1;
-  if (nctx_blocks > 0) {
-    const int64_t want = (kAttnTargetBlocks + B * H - 1) / (B * H);
-    nch = (int)std::min<int64_t>(std::max<int64_t>(want, 1), nctx_blocks);
-    nch = std::min(nch, kAttnMaxChunks);
-  }
-  p.chunk_blocks = nctx_blocks > 0 ? (int)((nctx_blocks + nch - 1) / nch) : 0;
-  p.nchunks = nctx_blocks > 0 ? (int)((nctx_blocks + p.chunk_blocks - 1) / p.chunk_blocks) : 1;
+  const int64_t ntot = (Lc + kAttnBlock - 1) / kAttnBlock + (Lt + kAttnBlock - 1) / kAttnBlock;
+  if (ntot == 0) return p;
+  const int64_t want = std::max<int64_t>(1, kAttnTargetBlocks / (B * H));
+  int64_t cb = (ntot + want - 1) / want;
+  if (const char *e = getenv("MTP_ATTN_CHUNK_BLOCKS")) cb = std::max<int64_t>(1, atoll(e));
+  cb = std::max(cb, (ntot + kAttnMaxChunks - 1) / kAttnMaxChunks);
+  p.chunk_blocks = (int)std::min<int64_t>(cb, ntot);
+  p.nchunks = (int)((ntot + p.chunk_blocks - 1) / p.chunk_blocks);
   if (p.nchunks > 1) {
     const int64_t qp = (int64_t)p.qt * 16;
     size_t off = kCounterBytes;
@@ -512,19 +515,24 @@ int launch_attention(AttnArgs &a, int ct, int64_t D, void *ws, size_t ws_bytes, 
                        (!a.vd || aligned16(a.vd));
   if (p.fast && strides8 && aligned) {
     if (p.total > 0 && (!ws || ws_bytes < p.total)) return MTP_ERR_WORKSPACE;
-    if (p.nchunks > 1 && (int64_t)a.B * a.H > kCounterSlots) return MTP_ERR_SHAPE;
-    AttnKernel k = attn_pick(ct, (int)D, p.qt);
-    if (!k) return MTP_ERR_DTYPE;
+    AttnKernel k = attn_pick(ct, (int)D);
+    AttnKernel km = attn_merge_pick(ct, (int)D);
+    if (!k || !km) return MTP_ERR_DTYPE;
     unsigned char *w8 = (unsigned char *)ws;
     a.nchunks = p.nchunks;
     a.chunk_blocks = p.chunk_blocks;
     if (p.nchunks > 1) {
       a.part = (float *)(w8 + p.part_off);
       a.ml = (float *)(w8 + p.ml_off);
-      a.ticket = (unsigned *)w8;
     }
     dim3 grid((unsigned)(a.B * a.H), (unsigned)p.nchunks, 1);
-    hipLaunchKernelGGL(k, grid, dim3(p.qt * 64), 0, st, a);
+    hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a);
+    if (p.nchunks > 1) {
+      int s = launch_status();
+      if (s != MTP_OK) return s;
+      hipLaunchKernelGGL(km, dim3((unsigned)(a.B * a.H), (unsigned)p.qt, 1), dim3((unsigned)D * 4),
+                         0, st, a);
+    }
     return launch_status();
   }
   if (D > 256) return MTP_ERR_SHAPE;

@@ -86,25 +86,6 @@ __device__ __forceinline__ void sk_lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned
 #endif
 }
 
-// f(integral_constant<int, I>) for I = LO .. HI - 1.
-template <int LO, int HI, class F>
-__device__ __forceinline__ void sk_static_for(F &&f) {
-  if constexpr (LO < HI) {
-    f(std::integral_constant<int, LO>{});
-    sk_static_for<LO + 1, HI>(f);
-  }
-}
-
-// Wait until at most N vector-memory loads of this wave are outstanding and
-// its LDS reads have returned, then meet the workgroup at a barrier; loads
-// of later stages stay in flight. The memory clobber keeps the compiler from
-// moving memory accesses across it.
-template <int N>
-__device__ __forceinline__ void sk_wait_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
 // ---------------------------------------------------------------------------
 // 1. prep: row m of x -> xn blocks
 template <int CT, bool FP8, bool GAM>
@@ -262,9 +243,9 @@ sk_kernel(const SkArgs a) {
   auto compute = [&](auto slotc, int nst_, auto nslotc) {
     constexpr int slot = decltype(slotc)::value;
     const unsigned char *base = lds + (slot & 1) * STAGE;
-    sk_static_for<0, KPW>([&](auto jc) {
+    static_for<0, KPW>([&](auto jc) {
       constexpr int jj = decltype(jc)::value;
-      sk_static_for<jj * NV / KPW, (jj + 1) * NV / KPW>([&](auto vc) { issue(vc, nst_, nslotc); });
+      static_for<jj * NV / KPW, (jj + 1) * NV / KPW>([&](auto vc) { issue(vc, nst_, nslotc); });
       const int j = wave * KPW + jj;  // k-step of the stage
       u32x4 av[2];
 #pragma unroll
@@ -300,12 +281,12 @@ sk_kernel(const SkArgs a) {
   // hoisted ahead of its phase would wait for loads issued just before, and
   // the prologue keeps the loop's load order (the wait counts at the loop
   // head are the minimum over both ways in).
-  sk_static_for<0, NS - 1>([&](auto pc) {
-    sk_static_for<0, NV>([&](auto vc) { issue(vc, decltype(pc)::value, pc); });
+  static_for<0, NS - 1>([&](auto pc) {
+    static_for<0, NV>([&](auto vc) { issue(vc, decltype(pc)::value, pc); });
     __builtin_amdgcn_sched_barrier(0);
   });
   w_to_lds(std::integral_constant<int, 0>{}, 0);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  lds_barrier();
   auto step = [&](auto rc, int s) {
     constexpr int r = decltype(rc)::value;  // s % NS
     __builtin_amdgcn_sched_barrier(0);
@@ -317,12 +298,12 @@ sk_kernel(const SkArgs a) {
     // stage s + NS - 1
     compute(rc, s + NS - 1, std::integral_constant<int, (r + NS - 1) % NS>{});
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    lds_barrier();
   };
   int s = 0;
   for (; s + NS <= nst; s += NS)
-    sk_static_for<0, NS>([&](auto rc) { step(rc, s + decltype(rc)::value); });
-  sk_static_for<0, NS - 1>([&](auto rc) {
+    static_for<0, NS>([&](auto rc) { step(rc, s + decltype(rc)::value); });
+  static_for<0, NS - 1>([&](auto rc) {
     if (s + decltype(rc)::value < nst) step(rc, s + decltype(rc)::value);
   });
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last stage

@@ -118,3 +118,49 @@ def test_tree_verify_step_full_size():
     y_ref = O.rmsnorm_linear(att_ref.reshape(64, -1), d["weight"], None, d["eps"], 1.0)
     ok, worst = close(y, y_ref, 2e-2)
     assert ok, f"linear worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("chunk_blocks", [1, 3, 5, 20, 36])
+def test_tree_verify_attention_chunkings(chunk_blocks, monkeypatch):
+    """Forced chunk lengths (blocks of 64 keys per workgroup) over 35 context
+    blocks plus 1 tree block: one block per chunk (36 partials merged), a
+    chunk that straddles the context / tree boundary (3), a tree-only chunk
+    (5), and chunks longer than the 1024-key page-table window (20, 36: the
+    window is reloaded mid-chunk)."""
+    from mtp_kernels import tree_verify_attention
+    from mtp_hip import workloads
+    monkeypatch.setenv("MTP_ATTN_CHUNK_BLOCKS", str(chunk_blocks))
+    g = torch.Generator().manual_seed(chunk_blocks)
+    N, H, Lc, D, ps = 64, 3, 2200, 128, 16
+    tm = workloads.draft_tree_mask(16, 4)[:N, :N]
+    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    vt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kp, vp, table = _paged(g, 1, H, Lc, D, ps, torch.bfloat16)
+    print(f"case tree-verify chunk_blocks={chunk_blocks}", flush=True)
+    out = tree_verify_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), ps,
+                                kt.to(DEV), vt.to(DEV), tm.to(DEV)).cpu()
+    ref = O.tree_verify_attention(q, kp, vp, table, ps, kt, vt, tm)
+    ok, worst = close(out, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("N,H,Lc,D,dtype", [(40, 2, 500, 64, torch.bfloat16),
+                                            (33, 4, 777, 128, torch.float16),
+                                            (17, 2, 64, 64, torch.float16)])
+def test_tree_verify_attention_head_dims_and_fp16(N, H, Lc, D, dtype):
+    from mtp_kernels import tree_verify_attention
+    from mtp_hip import workloads
+    g = torch.Generator().manual_seed(N * D + Lc)
+    ps = 16
+    tm = workloads.draft_tree_mask(16, 4)[:N, :N]
+    q = torch.randn(N, H, D, generator=g).to(dtype)
+    kt = torch.randn(N, H, D, generator=g).to(dtype)
+    vt = torch.randn(N, H, D, generator=g).to(dtype)
+    kp, vp, table = _paged(g, 1, H, Lc, D, ps, dtype)
+    print(f"case tree-verify N={N} H={H} Lc={Lc} D={D} {dtype}", flush=True)
+    out = tree_verify_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), ps,
+                                kt.to(DEV), vt.to(DEV), tm.to(DEV)).cpu()
+    ref = O.tree_verify_attention(q, kp, vp, table, ps, kt, vt, tm)
+    ok, worst = close(out, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
