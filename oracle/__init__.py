@@ -29,4 +29,9 @@ here, in tests/test_oracle.py):
   draft_tree — the reference's known shapes (32 nodes for depth 4 x 8
       branches; trunk mask rows) and ancestor closure.
   engine_rollback — the known-answer of generate_fused's consumer logic.
+  tree_attention / paged_attention / tree_verify_attention — float64 brute
+      force; all-ones mask equals plain softmax attention and an all-masked
+      row is NaN; paged equals contiguous keys under any page placement;
+      the tree-verify step equals one single-query tree_attention call per
+      node over context ++ tree keys (how the reference composes it).
 """
