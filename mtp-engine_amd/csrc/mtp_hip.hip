@@ -13,6 +13,7 @@
 #include "int4g_args.hpp"
 #include "quant.hpp"
 #include "sk_args.hpp"
+#include "skv_args.hpp"
 #include "ws_dispatch.hpp"
 
 using namespace mtp;
@@ -710,15 +711,77 @@ int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K, cons
 // ---------------------------------------------------------------------------
 static int verify_rows_per_chunk(int64_t seq) { return (int)((64 / seq) * seq); }
 
+// Persistent streaming verify (skv.hpp): 16-bit hidden and weights, no bias,
+// K a multiple of 512 (whole rounds of the 8-stage ring per tile), W within
+// the 2 GiB reach of one buffer descriptor. MTP_VERIFY_WSTREAM selects the
+// column-group kernel instead.
+constexpr size_t kSkvKeysBytes = 64 * 8;
+bool skv_usable(int ht, int64_t V, int64_t K, const void *bias) {
+  if (ht != MTP_BF16 && ht != MTP_F16) return false;
+  if (bias || K <= 0 || K % 512 != 0 || V <= 0) return false;
+  if (V * K * 2 >= ((int64_t)1 << 31)) return false;
+  const char *e = std::getenv("MTP_VERIFY_WSTREAM");
+  return !(e && *e);
+}
+
 size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq, int64_t V, int64_t K) {
   if (seq < 1 || seq > 64) return 0;
   Plan p = make_plan(h_dtype, h_dtype, rows, V, K, EPI_ARGMAX, verify_rows_per_chunk(seq));
-  return p.generic ? 0 : p.total;
+  const size_t wsb = p.generic ? 0 : p.total;
+  const size_t skv = (h_dtype == MTP_BF16 || h_dtype == MTP_F16) ? kCounterBytes + kSkvKeysBytes : 0;
+  return std::max(wsb, skv);
+}
+
+// One launch per chunk of rows_per_chunk rows (whole batch elements).
+static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const void *w, int64_t V,
+                      int rows_per_chunk, const WsArgs &o, void *ws, size_t ws_bytes,
+                      hipStream_t st) {
+  if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;
+  if (!ws || ws_bytes < kCounterBytes + kSkvKeysBytes) return MTP_ERR_WORKSPACE;
+  unsigned char *w8 = (unsigned char *)ws;
+  const int64_t ntiles = (V + kSkvBN - 1) / kSkvBN;
+  const int grid = (int)std::min<int64_t>(ntiles, kSkvBlocks);
+  for (int64_t m0 = 0; m0 < rows; m0 += rows_per_chunk) {
+    const int Mloc = (int)std::min<int64_t>(rows_per_chunk, rows - m0);
+    SkvKernel k = skv_pick(ht, Mloc <= 32 ? 1 : 2);
+    if (!k) return MTP_ERR_DTYPE;
+    SkvArgs a{};
+    a.x = (const uint16_t *)hidden + m0 * K;
+    a.w = w;
+    a.M = Mloc;
+    a.N = (int)V;
+    a.K = (int)K;
+    a.ntiles = (int)ntiles;
+    a.nst = (int)(K / 64);
+    a.keys = (unsigned long long *)(w8 + kCounterBytes);
+    a.ticket = (unsigned *)w8;
+    a.multi = o.multi;
+    if (!o.multi) {
+      a.draft = o.draft + m0;
+      a.accept = o.accept + m0;
+    } else {
+      const int64_t b0 = m0 / o.S_seq;
+      a.S_seq = o.S_seq;
+      a.D = o.D;
+      a.draft = o.draft ? o.draft + b0 * o.D : nullptr;
+      a.accept = o.accept ? o.accept + b0 * o.D : nullptr;
+      a.accepted_n = o.accepted_n + b0;
+      a.corrected = o.corrected + b0;
+    }
+    a.top = o.top ? o.top + m0 : nullptr;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(512), 0, st, a);
+    const int s = launch_status();
+    if (s != MTP_OK) return s;
+  }
+  return MTP_OK;
 }
 
 static int verify_common(const void *hidden, int ht, int64_t rows, int64_t K, const void *w,
                          int wt, int64_t V, const void *bias, int bt, int rows_per_chunk,
                          WsArgs &a, void *ws, size_t ws_bytes, void *stream) {
+  if (skv_usable(ht, V, K, bias))
+    return launch_skv(hidden, ht, rows, K, w, V, rows_per_chunk, a, ws, ws_bytes,
+                      (hipStream_t)stream);
   Plan p = make_plan(ht, wt, rows, V, K, EPI_ARGMAX, rows_per_chunk);
   if (p.generic) return MTP_ERR_SHAPE;
   if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;

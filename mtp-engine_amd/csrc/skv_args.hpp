@@ -1,0 +1,34 @@
+// Host-side view of the persistent verify GEMM (skv.hpp): arguments and
+// instantiation accessor.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mtp {
+
+constexpr int kSkvBlocks = 256;  // persistent workgroups: one per CU
+constexpr int kSkvBN = 256;      // columns per tile
+
+struct SkvArgs {
+  const void *x;        // hidden rows of this chunk: [M, K] compute type, row stride K
+  const void *w;        // [N, K] compute type
+  int M, N, K;          // M <= 64
+  int ntiles, nst;      // kSkvBN-column tiles, stages (64 k) per tile
+  unsigned long long *keys;  // [64] packed (value, index) maxima, zero between launches
+  unsigned *ticket;          // arrival ticket, zero between launches
+  // outputs (already offset to this chunk's rows / batch elements)
+  const int32_t *draft;  // [M] (single) or [M / S_seq, D] (multi)
+  int8_t *accept;
+  int32_t *accepted_n;
+  int32_t *corrected;
+  int32_t *top;  // [M] or null
+  int S_seq, D;
+  int multi;     // 1: chain acceptance, 0: single-token verify
+};
+
+typedef void (*SkvKernel)(SkvArgs);
+// Kernel for compute type ct (BF16 / F16) and mt 32-row tiles (1, 2), or null.
+SkvKernel skv_pick(int ct, int mt);
+
+}  // namespace mtp

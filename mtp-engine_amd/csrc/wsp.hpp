@@ -157,7 +157,7 @@ wsp_kernel(const WsArgs a) {
     const uint32_t adv = (uint32_t)unit * 64u;
     const __amdgpu_buffer_rsrc_t r = make_rsrc(wbase + adv, unit < u_kg1 ? w_bytes - adv : 0u);
 #pragma unroll
-    for (int u = 0; u < NSUB; ++u) wr[u] = bload16(r, wvo[u]);
+    for (int u = 0; u < NSUB; ++u) wr[u] = bload16_nt(r, wvo[u]);
   };
   auto load_x = [&](u32x4 (&xr)[XW], int s) {
     const int unit = u_kg0 + s;

@@ -103,6 +103,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// Streaming (non-temporal) variant for data read once: weights.
+__device__ __forceinline__ u32x4 bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past any descriptor's range
 // Cache-policy operand of the buffer intrinsics selecting sc1: the same
 // agent-coherent access the compiler emits for agent-scope atomic loads and
@@ -182,7 +186,7 @@ wstream_kernel(const WsArgs a) {
       const bool ok = (kb < kbB) && (kb * KB + (4 * j + lg) * WE < K);
       const uint32_t koff = (uint32_t)kb * KB * Sh::kWBytes + j * 64;
 #pragma unroll
-      for (int u = 0; u < NSUB; ++u) wr[u][j] = bload16(wrs, ok ? wrow[u] + koff : kOOB);
+      for (int u = 0; u < NSUB; ++u) wr[u][j] = bload16_nt(wrs, ok ? wrow[u] + koff : kOOB);
     }
   };
 

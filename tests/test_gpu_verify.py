@@ -172,3 +172,80 @@ def test_multi_verify_workload_full_size():
     got = O.engine_rollback(out[0], out[1], out[2], draft)
     exp = O.engine_rollback(ra, rn, rc, draft)
     assert got[:2] == exp[:2] and torch.equal(got[2], exp[2])
+
+
+# --- the persistent streaming path: 16-bit, no bias, K % 512 == 0 ---------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K,V", [(1, 512, 3000), (33, 1024, 50257), (64, 512, 20000),
+                                   (70, 512, 128), (5, 2048, 70000)])
+def test_fused_verify_streaming_path(dtype, M, K, V):
+    """Row chunks of 64 (70 rows: two launches), tiles past V (V % 64 != 0),
+    grids smaller than the persistent 256 (V = 128, 3000)."""
+    import mtp_fused_verify as FV
+    g = torch.Generator().manual_seed(M * 7 + V)
+    h = torch.randn(M, K, generator=g).to(dtype)
+    W = (0.05 * torch.randn(V, K, generator=g)).to(dtype)
+    top_ref, gap = O.logits_top(h, W)
+    draft = top_ref.clone().to(torch.int64)
+    draft[::3] = (draft[::3] + 1) % V
+    print(f"case verify-stream dtype={dtype} M={M} K={K} V={V}", flush=True)
+    acc, top = FV.fused_verify(h.to(DEV), W.to(DEV), draft.to(DEV))
+    torch.cuda.synchronize()
+    _check_tokens(top, top_ref, gap, 1e-3)
+    sure = gap > 1e-3
+    exp_acc = (top_ref == draft.to(torch.int32)).to(torch.int8)
+    assert torch.equal(acc.cpu()[sure], exp_acc[sure])
+
+
+def test_verify_streaming_planted_ties_and_nan():
+    """Ties between columns handled by different workgroups and tiles: the
+    lowest index wins; a NaN logit is the maximum; all-zero logits give 0."""
+    from mtp_hip import ops
+    V, K = 40000, 512
+    W = torch.zeros(V, K)
+    W[10, :] = 1.0 / 64
+    W[650, :] = 1.0 / 64     # another tile of another workgroup
+    W[39999, :] = 1.0 / 64   # the last, partial tile
+    h = torch.ones(3, K)
+    h[2] = -1.0
+    Wb = W.to(torch.bfloat16)
+    acc, top = ops.verify(h.to(torch.bfloat16).to(DEV), Wb.to(DEV), torch.tensor([10, 0, 0]).to(DEV))
+    assert top.cpu().tolist() == [10, 10, 0]
+    assert acc.cpu().tolist() == [1, 0, 1]
+    Wn = Wb.clone()
+    Wn[33333, 7] = float("nan")
+    _, topn = ops.verify(h.to(torch.bfloat16).to(DEV), Wn.to(DEV), torch.zeros(3, dtype=torch.int64).to(DEV))
+    assert topn.cpu().tolist() == [33333, 33333, 33333]
+    z = torch.zeros(2, K, dtype=torch.bfloat16)
+    _, topz = ops.verify(z.to(DEV), Wn.to(DEV), torch.zeros(2, dtype=torch.int64).to(DEV))
+    assert topz.cpu().tolist() == [33333, 33333]  # 0 * NaN is NaN
+    _, topz = ops.verify(z.to(DEV), Wb.to(DEV), torch.zeros(2, dtype=torch.int64).to(DEV))
+    assert topz.cpu().tolist() == [0, 0]
+
+
+@pytest.mark.parametrize("B,D,K,V", [(8, 4, 1024, 30000), (13, 4, 512, 5000), (4, 0, 512, 777)])
+def test_multi_verify_streaming_path(B, D, K, V):
+    """13 x 5 = 65 rows: two row chunks (60 + 5) in two launches."""
+    from mtp_hip import ops
+    hidden, W, b, draft, _, _ = _chain_case(B, D, K, V, torch.bfloat16, seed=B + K + V, bias=False)
+    print(f"case multi-stream B={B} D={D} K={K} V={V}", flush=True)
+    out = ops.multi_verify(hidden.to(DEV), W.to(DEV), draft.to(DEV), None, return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hidden, W, b, draft, 1e-3)
+
+
+def test_verify_streaming_and_column_group_paths_agree(monkeypatch):
+    """The persistent streaming kernel and the column-group kernel
+    (MTP_VERIFY_WSTREAM) give the same tokens wherever the top-2 gap is clear."""
+    from mtp_hip import ops
+    hidden, W, _, draft, top, gap = _chain_case(6, 4, 1024, 60000, torch.bfloat16, seed=5,
+                                                bias=False)
+    hd, Wd, dd = hidden.to(DEV), W.to(DEV), draft.to(DEV)
+    a = ops.multi_verify(hd, Wd, dd, None, return_top=True)
+    monkeypatch.setenv("MTP_VERIFY_WSTREAM", "1")
+    b = ops.multi_verify(hd, Wd, dd, None, return_top=True)
+    torch.cuda.synchronize()
+    sure = (gap > 1e-3).reshape(-1)
+    assert torch.equal(a[3].cpu().reshape(-1)[sure], b[3].cpu().reshape(-1)[sure])
+    assert torch.equal(a[3].cpu().reshape(-1)[sure], top.reshape(-1)[sure].to(torch.int32))
