@@ -34,6 +34,10 @@
 //     g = lane / 32 holds k 16 g .. 16 g + 15, the first 8 in k-step 2p, the
 //     other 8 in k-step 2p + 1 (16-bit W: k-step j, lane group g holds
 //     k 16 j + 8 g .. + 7); the prep writes xn in the same order.
+//  The stages of a split are taken starting at 7 tile mod (stages): tiles in
+//  step with each other then read different 128-byte offsets of their rows,
+//  which spreads the requests over the HBM channels (the same offset of every
+//  row at once concentrates them on few channels).
 //  End: S == 1 applies the epilogue directly; otherwise the workgroups of a
 //  tile hand fp32 partial sums to the last one to arrive (coherent stores,
 //  arrival ticket; see the hand-off notes in mtp_common.hpp), which sums them
@@ -206,19 +210,24 @@ sk_kernel(const SkArgs a) {
   }
   u32x4 xr[NS][NXL];   // xn register ring
   u32x4 wr[NS][NWC];   // W register ring
+  // The split's stages are taken starting at 7 tile mod nst: workgroups in
+  // step with each other then read different 128-byte offsets of their W
+  // rows, which spreads the requests over the HBM channels.
+  const int rot = (7 * tile) % nst;
 
   // Instruction v (0 <= v < NV) of stage st into ring slot `slot`. Stages
   // past the split read zeros or other stages' bytes into a slot that is
   // never computed on, so the count of instructions per stage is always NV.
   auto issue = [&](auto vc, int st, auto slotc) {
     constexpr int v = decltype(vc)::value, slot = decltype(slotc)::value;
+    const int str = st < nst ? (st + rot < nst ? st + rot : st + rot - nst) : st;
     if constexpr (v < NWC) {
       wr[slot][v] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[v], st * kSkUB, 2));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[v], str * kSkUB, 2));
     } else {
       constexpr int i = v - NWC;
       xr[slot][i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i], st * KS * 1024, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i], str * KS * 1024, 0));
     }
   };
 
