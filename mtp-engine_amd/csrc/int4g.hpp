@@ -234,7 +234,9 @@ int4_gemm_kernel(const I4Args a) {
 
   const int th = threadIdx.x;
   const int lane = th & 63;
-  const int wave = th >> 6;
+  // the wave index is uniform: readfirstlane keeps the scale copy's scalar
+  // offset (which depends on it) in scalar registers, without a waterfall
+  const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
   const int h = lane >> 5, l32 = lane & 31;
 
   // blockIdx -> (column group, row group): the row groups of column group
