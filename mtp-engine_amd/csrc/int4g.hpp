@@ -291,19 +291,26 @@ int4_gemm_kernel(const I4Args a) {
 
   // Vector-memory instruction v (0 <= v < NV) of unit `unit` into LDS
   // stage `slot`: weight copies first, then the scale copy, then x copies.
+  // Units past the last one copy with an out-of-range vector offset: zeros,
+  // no memory access (the scalar offset is not part of the descriptor's
+  // range check).
   auto issue = [&](auto vc, int unit, int slot) {
     constexpr int v = decltype(vc)::value;
+    const bool live = unit < nunits;
+    const int su = live ? unit : 0;
     if constexpr (v < NWL) {
-      lds_copy16(wrs, xs + slot * STAGE + XST + (wave + 4 * v) * 1024, wvo[v], unit * 64);
+      lds_copy16(wrs, xs + slot * STAGE + XST + (wave + 4 * v) * 1024, live ? wvo[v] : kOOB,
+                 su * 64);
     } else if constexpr (v == NWL) {
-      const int k = unit * UK + 32 * wave;
+      const int k = su * UK + 32 * wave;
       const int g = a.glog >= 0 ? k >> a.glog : k / a.group;
-      lds_copy16(srs, xs + slot * STAGE + XST + WST + wave * 1024, svo, (int)((uint32_t)g * ldst2));
+      lds_copy16(srs, xs + slot * STAGE + XST + WST + wave * 1024, live ? svo : kOOB,
+                 (int)((uint32_t)g * ldst2));
     } else {
       const int i = v - NWL - 1;
       const int c = wave + 4 * i;
-      lds_copy16(xrs, xs + slot * STAGE + (c >> 3) * TILE + (c & 7) * 1024, xvo[i],
-                 unit * TILE);
+      lds_copy16(xrs, xs + slot * STAGE + (c >> 3) * TILE + (c & 7) * 1024, live ? xvo[i] : kOOB,
+                 su * TILE);
     }
   };
 
@@ -385,10 +392,9 @@ int4_gemm_kernel(const I4Args a) {
   // Pipeline: units u + 1 and u + 2 are in flight while unit u computes.
   // The loop is unrolled by the ring length so that stage r's offsets are
   // compile-time constants. Copies are issued for every u + 2, also past
-  // the last unit: such a copy reads zeros (past the end of its
-  // descriptor) or bytes of another tile or row, into a stage that is
-  // never computed on, so the count of instructions behind the copies of
-  // unit u is always NV.
+  // the last unit: such a copy writes zeros into a stage that is never
+  // computed on, so the count of instructions behind the copies of unit u
+  // is always NV.
   static_for<0, NV>([&](auto vc) { issue(vc, 0, 0); });
   __builtin_amdgcn_sched_barrier(0);  // every copy of unit 0 before any of unit 1
   static_for<0, NV>([&](auto vc) { issue(vc, 1, 1); });

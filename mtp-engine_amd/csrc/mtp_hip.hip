@@ -13,6 +13,7 @@
 #include "int4g_args.hpp"
 #include "quant.hpp"
 #include "sk_args.hpp"
+#include "skl_args.hpp"
 #include "skv_args.hpp"
 #include "ws_dispatch.hpp"
 
@@ -396,6 +397,99 @@ int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Single-launch skinny plan (skl.hpp): at most 64 rows of 16-bit x, W of fp8
+// or the same 16-bit type, whole 128-byte stages per W row, the norm folded
+// into the GEMM. Tiles of 32 nw columns; K-splits until the grid covers the
+// CUs once. Workspace: counters, split-K partial tiles and sums of squares.
+struct PlanSkl {
+  bool ok = false;
+  int ct = 0, wt = 0, mt = 0, nw = 8;
+  bool gam = false;
+  int G = 0, S = 1, kb_per = 0, nkb = 0;
+  size_t part_off = 0, ss_off = 0, total = 0;
+};
+
+constexpr int kSklCUs = 256;  // compute units of the device (one workgroup each)
+
+// MTP_SKL=1 forces the single-launch kernel wherever it applies, MTP_SKL=0
+// turns it off; by default it runs where its 256-column tiles fill the CUs
+// without a K-split (N > 128 * 256): a split's hand-off through the device
+// coherence point (partial stores, arrival ticket, partial loads) costs
+// about 7 us at the end of the launch, more than the x traffic it saves.
+// Measured, fp8 W, K 4096: M 64 N 131072 144 us vs 174 us (tiled 64-column
+// kernel), M 16 N 131072 95 us vs 153 us; M 64 N 14336 (four splits) 27.8
+// us vs 25.7 us.
+int skl_mode() {
+  const char *e = std::getenv("MTP_SKL");
+  if (!e || !*e) return -1;
+  return *e == '0' ? 0 : 1;
+}
+
+PlanSkl make_plan_skl(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
+  PlanSkl p;
+  p.ct = ct;
+  p.wt = wt;
+  p.gam = gam;
+  if (ct != MTP_BF16 && ct != MTP_F16) return p;
+  if (wt != MTP_FP8E4M3 && wt != ct) return p;
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0) return p;
+  const int wb = dtype_bytes(wt);
+  if ((K * wb) % kSkUB != 0) return p;
+  const char *nwe = std::getenv("MTP_SKL_WAVES");
+  if (nwe && *nwe) p.nw = std::atoi(nwe) == 4 ? 4 : 8;
+  const int64_t bn = skl_bn(p.nw);
+  // buffer descriptors: x, the workgroup's W rows (32-bit sizes and offsets)
+  if (M * K * 2 >= ((int64_t)1 << 31) || bn * K * wb >= ((int64_t)1 << 31)) return p;
+  p.mt = M <= 32 ? 1 : 2;
+  p.G = (int)((N + bn - 1) / bn);
+  p.nkb = (int)(K * wb / kSkUB);
+  const int uk = kSkUB / wb;  // k per stage
+  int S = 1;
+  const char *force = std::getenv("MTP_SKL_SPLITS");
+  if (force && *force) S = std::max(1, std::atoi(force));
+  else S = std::max(1, kSklCUs / std::max(1, p.G));
+  if (S > p.nkb) S = p.nkb;
+  for (;;) {
+    p.kb_per = (p.nkb + S - 1) / S;
+    if (!gam || (int64_t)p.kb_per * uk <= kSklGammaMax || S >= p.nkb) break;
+    ++S;
+  }
+  if (gam && (int64_t)p.kb_per * uk > kSklGammaMax) return p;
+  p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  if ((int64_t)p.G * p.S > INT32_MAX) return p;
+  if (p.S > 1 && p.G > kCounterSlots) return p;
+  size_t off = kCounterBytes;
+  if (p.S > 1) {
+    const size_t part = (size_t)p.S * p.G * skl_tile_bytes(p.mt, p.nw);
+    if (part >= ((size_t)1 << 31)) return p;
+    p.part_off = off;
+    off += align_up(part, 256);
+    p.ss_off = off;
+    off += align_up((size_t)p.S * p.G * 64 * sizeof(float), 256);
+  }
+  p.total = off;
+  p.ok = skl_pick(ct, wt, p.mt, p.nw, gam) != nullptr;
+  return p;
+}
+
+int launch_skl(const PlanSkl &p, SklArgs &a, void *ws, hipStream_t st) {
+  SklKernel k = skl_pick(p.ct, p.wt, p.mt, p.nw, p.gam);
+  if (!k) return MTP_ERR_DTYPE;
+  unsigned char *w8 = (unsigned char *)ws;
+  a.G = p.G;
+  a.S = p.S;
+  a.kb_per = p.kb_per;
+  a.nkb = p.nkb;
+  if (p.S > 1) {
+    a.part = (float *)(w8 + p.part_off);
+    a.part_ss = (float *)(w8 + p.ss_off);
+    a.ticket = (unsigned *)w8;
+  }
+  hipLaunchKernelGGL(k, dim3((unsigned)(p.G * p.S)), dim3((unsigned)(64 * p.nw)), 0, st, a);
+  return launch_status();
+}
+
 int launch_generic_linear(const void *x, int xt, const void *w, int wt, const float *wscale,
                           const void *i4scale, int i4dt, int group, int nib, const void *gamma,
                           int gt, const void *bias, int bt, void *y, int64_t M, int64_t N,
@@ -438,6 +532,28 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
+  const int sklm = skl_mode();
+  if (sklm != 0) {
+    const PlanSkl pl = make_plan_skl(xt, wt, M, N, K, gamma != nullptr);
+    if (pl.ok && (sklm == 1 || pl.S == 1) && aligned && (!gamma || gt == MTP_F32)) {
+      if (!ws || ws_bytes < pl.total) return MTP_ERR_WORKSPACE;
+      SklArgs la{};
+      la.x = x;
+      la.gamma = (const float *)gamma;
+      la.w = w;
+      la.wscale = wscale;
+      la.bias = bias;
+      la.bias_dt = bt;
+      la.y = y;
+      la.M = (int)M;
+      la.N = (int)N;
+      la.K = (int)K;
+      la.norm = norm;
+      la.eps = eps;
+      la.scale = scale;
+      return launch_skl(pl, la, ws, st);
+    }
+  }
   const PlanSk ps = make_plan_sk(xt, wt, M, N, K, gamma != nullptr);
   if (ps.ok && aligned && (!gamma || gt == MTP_F32)) {
     if (!ws || ws_bytes < ps.total) return MTP_ERR_WORKSPACE;
@@ -661,6 +777,8 @@ size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, in
     if (p.ok && p.total > most) most = p.total;
     PlanSk q = make_plan_sk(x_dtype, w_kind, M, N, K, gam != 0);
     if (q.ok && q.total > most) most = q.total;
+    PlanSkl l = make_plan_skl(x_dtype, w_kind, M, N, K, gam != 0);
+    if (l.ok && l.total > most) most = l.total;
   }
   return most;
 }

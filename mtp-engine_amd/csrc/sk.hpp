@@ -90,6 +90,36 @@ __device__ __forceinline__ void sk_lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned
 #endif
 }
 
+// Epilogue factors of the 16 output columns n0c + 8 g + j (g, j < 4) one
+// lane stores: wscale[n] (1 without wscale) and bias[n] (0 without bias),
+// loaded in one batch through buffer descriptors (columns >= N read 0).
+// Issued at the start of a kernel, their latency hides behind its main
+// loop; a load placed between output stores that might alias it would wait
+// for its own round trip.
+__device__ __forceinline__ void load_col_factors(const float *wscale, const void *bias,
+                                                 int bias_dt, int N, int n0c, float (&ws)[16],
+                                                 float (&bi)[16]) {
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(wscale, wscale ? (uint32_t)N * 4u : 0u);
+  const uint32_t bb = bias_dt == MTP_F32 ? 4u : 2u;
+  const __amdgpu_buffer_rsrc_t br = make_rsrc(bias, bias ? (uint32_t)N * bb : 0u);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t n = (uint32_t)(n0c + 8 * (i >> 2) + (i & 3));
+    ws[i] = 1.0f;
+    bi[i] = 0.f;
+    if (wscale)
+      ws[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, n * 4u, 0, 0));
+    if (bias) {
+      if (bias_dt == MTP_F32) {
+        bi[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, n * 4u, 0, 0));
+      } else {
+        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(br, n * 2u, 0, 0);
+        bi[i] = bias_dt == MTP_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 1. prep: row m of x -> xn blocks
 template <int CT, bool FP8, bool GAM>
@@ -181,6 +211,11 @@ sk_kernel(const SkArgs a) {
   // blockIdx -> (column tile, split): the splits of a tile are consecutive
   const int tile = (int)blockIdx.x / a.S, sp = (int)blockIdx.x - tile * a.S;
   const int n0 = tile * kSkBN;
+  // end-phase owner of this wave (see below) and its column factors
+  const int ou = wave & 1, ot = wave >> 1;
+  const bool owner = ot < MT;
+  float cws[16], cbi[16];
+  load_col_factors(a.wscale, a.bias, a.bias_dt, N, n0 + 32 * ou + 4 * (lane >> 5), cws, cbi);
   const int st0 = sp * a.kb_per;
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // stages of this split (>= 1)
 
@@ -216,18 +251,22 @@ sk_kernel(const SkArgs a) {
   const int rot = (7 * tile) % nst;
 
   // Instruction v (0 <= v < NV) of stage st into ring slot `slot`. Stages
-  // past the split read zeros or other stages' bytes into a slot that is
-  // never computed on, so the count of instructions per stage is always NV.
+  // past the split load with an out-of-range vector offset: zeros, no memory
+  // access (the scalar offset is not part of the descriptor's range check),
+  // into a slot that is never computed on, so the count of instructions per
+  // stage is always NV.
   auto issue = [&](auto vc, int st, auto slotc) {
     constexpr int v = decltype(vc)::value, slot = decltype(slotc)::value;
-    const int str = st < nst ? (st + rot < nst ? st + rot : st + rot - nst) : st;
+    const bool live = st < nst;
+    const int str = live ? (st + rot < nst ? st + rot : st + rot - nst) : 0;
     if constexpr (v < NWC) {
       wr[slot][v] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[v], str * kSkUB, 2));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, live ? wvo[v] : kOOB, str * kSkUB, 2));
     } else {
       constexpr int i = v - NWC;
       xr[slot][i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i], str * KS * 1024, 0));
+          u32x4,
+          __builtin_amdgcn_raw_buffer_load_b128(xrs, live ? xvo[i] : kOOB, str * KS * 1024, 0));
     }
   };
 
@@ -326,8 +365,6 @@ sk_kernel(const SkArgs a) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) red[((wave * 2 + u) * MT + t) * 64 + lane] = acc[u][t];
   __syncthreads();
-  const int ou = wave & 1, ot = wave >> 1;
-  const bool owner = ot < MT;
   f32x16 v;
 #pragma unroll
   for (int e = 0; e < 16; ++e) v[e] = 0.f;
@@ -346,13 +383,9 @@ sk_kernel(const SkArgs a) {
       const int n = n0 + 32 * ou + 8 * g + 4 * ag;
       float o[4];
 #pragma unroll
-      for (int jx = 0; jx < 4; ++jx) {
-        const int nn = min(n + jx, N - 1);
-        float x = r[4 * g + jx];
-        if (a.wscale) x *= a.wscale[nn];
-        if (a.bias) x += load_as_f32(a.bias, a.bias_dt, nn);
-        o[jx] = x * a.scale;
-      }
+      for (int jx = 0; jx < 4; ++jx)
+        o[jx] = (a.bias ? r[4 * g + jx] * cws[4 * g + jx] + cbi[4 * g + jx]
+                        : r[4 * g + jx] * cws[4 * g + jx]) * a.scale;
       const int64_t yb = (int64_t)m * N + n;
       if (n + 3 < N && (N & 3) == 0) {
         uint2 pk;

@@ -19,7 +19,8 @@ DEV = "cuda"
 
 @pytest.fixture(autouse=True)
 def _tune_reset():
-    old = {k: os.environ.pop(k, None) for k in ("MTP_WS_TUNE", "MTP_SK_SPLITS")}
+    old = {k: os.environ.pop(k, None)
+           for k in ("MTP_WS_TUNE", "MTP_SK_SPLITS", "MTP_SKL", "MTP_SKL_SPLITS", "MTP_SKL_WAVES")}
     yield
     for k, v in old.items():
         os.environ.pop(k, None)
@@ -178,6 +179,58 @@ def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
     for out, r in ((y, ref), (y2, ref2)):
         ok, worst = close(out, r, 2e-2)
         assert ok, f"worst err/bound = {worst:.3g}"
+
+
+SKL_CASES = [(None, "8", (40, 40000, 512)), (None, "8", (3, 33024, 256)),
+             ("1", "4", (64, 1000, 2048)), ("1", "8", (7, 300, 512)),
+             ("2", "8", (33, 260, 1024)), ("3", "4", (1, 128, 1280)),
+             ("5", "8", (64, 2000, 2048)), (None, "4", (17, 520, 768))]
+
+
+@pytest.mark.parametrize("splits,waves,shape", SKL_CASES)
+@pytest.mark.parametrize("wkind", ["fp8", "same"])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
+    """The single-launch skinny kernel (norm applied to the fp32 sums,
+    gamma applied while x is staged, 32 * waves columns per workgroup):
+    forced everywhere (MTP_SKL=1) for the small shapes, by default for the
+    wide ones (no K-split), with forced and planned K-splits, ragged M and
+    N, with and without gamma, bias and norm, against the oracle."""
+    M, N, K = shape
+    if N <= 32768:
+        os.environ["MTP_SKL"] = "1"
+    if splits is not None:
+        os.environ["MTP_SKL_SPLITS"] = splits
+    os.environ["MTP_SKL_WAVES"] = waves
+    from mtp_hip import ops
+    print(f"case skl splits={splits} waves={waves} M={M} N={N} K={K} w={wkind} x={xdtype}",
+          flush=True)
+    g = torch.Generator().manual_seed(M * 17 + N + K)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(xdtype)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+        y2 = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), None, 1e-6, norm=False)
+        ref2 = O.rmsnorm_linear_fp8(x, wq, ws, None, 1e-6, norm=False)
+    else:
+        Wc = W.to(xdtype)
+        y = ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5, gamma=gm)
+        y2 = ops.rmsnorm_linear(_dev(x), _dev(Wc), None, 1e-6, 1.0, norm=False)
+        ref2 = O.rmsnorm_linear(x, Wc, None, 1e-6, 1.0, norm=False)
+    torch.cuda.synchronize()
+    for out, r in ((y, ref), (y2, ref2)):
+        ok, worst = close(out, r, 2e-2)
+        assert ok, f"worst err/bound = {worst:.3g}"
+    # deterministic: fixed split and row-sum orders
+    y3 = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm)) \
+        if wkind == "fp8" else ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5,
+                                                  gamma=_dev(gm))
+    assert torch.equal(y, y3)
 
 
 @pytest.mark.parametrize("M", [8, 32, 64])
