@@ -251,6 +251,17 @@ int4_gemm_kernel(const I4Args a) {
   }
   if (cg >= a.gn) return;
   const int n0 = cg * BN;
+  // row factors of the epilogue, loaded now so that their latency hides
+  // behind the main loop (rows past the padded tile read 0 and are not stored)
+  float omr[MT];
+  {
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(a.omul, (uint32_t)a.M * 4u);
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+      omr[j] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(
+                     ors, (uint32_t)(rg * MT * 32 + 32 * j + (threadIdx.x & 31)) * 4u, 0, 0));
+  }
   const int nunits = a.K / UK;
 
   // Weights: per unit the workgroup's BN rows x 64 bytes are copied to LDS
@@ -294,7 +305,7 @@ int4_gemm_kernel(const I4Args a) {
   // Units past the last one copy with an out-of-range vector offset: zeros,
   // no memory access (the scalar offset is not part of the descriptor's
   // range check).
-  auto issue = [&](auto vc, int unit, int slot) {
+  auto issue = [&](auto vc, int unit, int slot) __attribute__((always_inline)) {
     constexpr int v = decltype(vc)::value;
     const bool live = unit < nunits;
     const int su = live ? unit : 0;
@@ -330,7 +341,7 @@ int4_gemm_kernel(const I4Args a) {
   // The NV vector-memory instructions of unit `nunit` (two units ahead) are
   // spread over the k-steps so that the memory pipeline's queues never fill
   // and block the in-order issue of the MFMAs behind them.
-  auto compute = [&](int slot, int nunit, int nslot) {
+  auto compute = [&](int slot, int nunit, int nslot) __attribute__((always_inline)) {
     const unsigned char *sx = xs + slot * STAGE + lane * 16;
     const unsigned char *sw = xs + slot * STAGE + XST;
     const unsigned char *ss = xs + slot * STAGE + XST + WST;
@@ -347,7 +358,7 @@ int4_gemm_kernel(const I4Args a) {
         const _Float16 f = *(const _Float16 *)(ss + (2 * h + g) * 1024 + wcol[t] * 2);
         s2[t][g] = h2{f, f};
       }
-    auto decode = [&](h8 (&af)[NA], int s) {
+    auto decode = [&](h8 (&af)[NA], int s) __attribute__((always_inline)) {
 #pragma unroll
       for (int t = 0; t < NA; ++t) {
         const uint32_t w = wr[t][s >> 2][s & 3] ^ flip;
@@ -365,7 +376,7 @@ int4_gemm_kernel(const I4Args a) {
         af[t] = __builtin_bit_cast(h8, o);
       }
     };
-    auto read_b = [&](h8 (&bv)[MT], int s) {
+    auto read_b = [&](h8 (&bv)[MT], int s) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < MT; ++j) bv[j] = *(const h8 *)(sx + j * TILE + s * 1024);
     };
@@ -398,7 +409,7 @@ int4_gemm_kernel(const I4Args a) {
   static_for<0, NV>([&](auto vc) { issue(vc, 0, 0); });
   __builtin_amdgcn_sched_barrier(0);  // every copy of unit 0 before any of unit 1
   static_for<0, NV>([&](auto vc) { issue(vc, 1, 1); });
-  auto step = [&](auto rc, int u) {
+  auto step = [&](auto rc, int u) __attribute__((always_inline)) {
     constexpr int r = decltype(rc)::value;
     __builtin_amdgcn_sched_barrier(0);
     // this wave's copies of unit u have landed once at most the NV
@@ -427,7 +438,7 @@ int4_gemm_kernel(const I4Args a) {
   for (int j = 0; j < MT; ++j) {
     const int m = m0 + 32 * j + l32;
     if (m >= a.M) continue;
-    const float om = a.omul[m];
+    const float om = omr[j];
 #pragma unroll
     for (int t = 0; t < NA; ++t) {
 #pragma unroll

@@ -687,8 +687,10 @@ size_t int4_xn_bytes(int64_t M, int64_t K) {
   return align_up((size_t)int4_tiles(M).rows * K * 2, 256);
 }
 size_t int4_omul_bytes(int64_t M) { return align_up((size_t)int4_tiles(M).rows * 4, 256); }
+// Workspace: the counter region (left untouched: other entry points keep
+// their arrival tickets there), then xn, omul and the transposed scales.
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t ng) {
-  return int4_xn_bytes(M, K) + int4_omul_bytes(M) +
+  return kCounterBytes + int4_xn_bytes(M, K) + int4_omul_bytes(M) +
          align_up((size_t)ng * int4_ldst(M, N) * 2, 256);
 }
 constexpr int64_t kInt4MaxK = (int64_t)1 << 23;  // keeps every buffer offset in 32 bits
@@ -712,7 +714,7 @@ int launch_int4(const void *x, int xdt, int64_t M, int64_t K, const uint8_t *pac
   const int64_t blocks = (gn + 7) / 8 * 8 * tl.gm;
   const int64_t sblocks = (N + 63) / 64;  // scale-transpose blocks of the prep launch
   if (blocks > INT32_MAX || tl.rows + sblocks > INT32_MAX) return MTP_ERR_SHAPE;
-  unsigned char *w8 = (unsigned char *)ws;
+  unsigned char *w8 = (unsigned char *)ws + kCounterBytes;
   I4Args a;
   a.xn = w8;
   a.omul = (const float *)(w8 + int4_xn_bytes(M, K));

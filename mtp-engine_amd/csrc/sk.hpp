@@ -90,36 +90,6 @@ __device__ __forceinline__ void sk_lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned
 #endif
 }
 
-// Epilogue factors of the 16 output columns n0c + 8 g + j (g, j < 4) one
-// lane stores: wscale[n] (1 without wscale) and bias[n] (0 without bias),
-// loaded in one batch through buffer descriptors (columns >= N read 0).
-// Issued at the start of a kernel, their latency hides behind its main
-// loop; a load placed between output stores that might alias it would wait
-// for its own round trip.
-__device__ __forceinline__ void load_col_factors(const float *wscale, const void *bias,
-                                                 int bias_dt, int N, int n0c, float (&ws)[16],
-                                                 float (&bi)[16]) {
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(wscale, wscale ? (uint32_t)N * 4u : 0u);
-  const uint32_t bb = bias_dt == MTP_F32 ? 4u : 2u;
-  const __amdgpu_buffer_rsrc_t br = make_rsrc(bias, bias ? (uint32_t)N * bb : 0u);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t n = (uint32_t)(n0c + 8 * (i >> 2) + (i & 3));
-    ws[i] = 1.0f;
-    bi[i] = 0.f;
-    if (wscale)
-      ws[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, n * 4u, 0, 0));
-    if (bias) {
-      if (bias_dt == MTP_F32) {
-        bi[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, n * 4u, 0, 0));
-      } else {
-        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(br, n * 2u, 0, 0);
-        bi[i] = bias_dt == MTP_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // 1. prep: row m of x -> xn blocks
 template <int CT, bool FP8, bool GAM>
@@ -215,7 +185,7 @@ sk_kernel(const SkArgs a) {
   const int ou = wave & 1, ot = wave >> 1;
   const bool owner = ot < MT;
   float cws[16], cbi[16];
-  load_col_factors(a.wscale, a.bias, a.bias_dt, N, n0 + 32 * ou + 4 * (lane >> 5), cws, cbi);
+  load_col_factors<4>(a.wscale, a.bias, a.bias_dt, N, n0 + 32 * ou + 4 * (lane >> 5), 8, cws, cbi);
   const int st0 = sp * a.kb_per;
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // stages of this split (>= 1)
 

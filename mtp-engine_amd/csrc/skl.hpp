@@ -97,7 +97,7 @@ skl_kernel(const SklArgs a) {
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // stages of this split (>= 1)
   const int rot = (7 * b) % nst;
   float cws[16], cbi[16];  // epilogue factors of the lane's 16 columns
-  load_col_factors(a.wscale, a.bias, a.bias_dt, N, n0 + 32 * wave + 4 * ag, cws, cbi);
+  load_col_factors<4>(a.wscale, a.bias, a.bias_dt, N, n0 + 32 * wave + 4 * ag, 8, cws, cbi);
   // stage of the split taken at position st < nst
   auto rotated = [&](int st) __attribute__((always_inline)) {
     return st + rot < nst ? st + rot : st + rot - nst;

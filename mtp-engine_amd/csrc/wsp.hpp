@@ -117,6 +117,21 @@ wsp_kernel(const WsArgs a) {
   const int Mloc = min(a.rows_per_chunk, a.M - m0);
   const int K = a.K, N = a.N;
 
+  // Output quads: item = m + MPAD q holds columns 4 q .. 4 q + 3 of row m of
+  // the tile; thread th stores items th + NT i. Their epilogue factors are
+  // loaded in one batch before the stores (held through the main loop they
+  // would cost registers the pipeline needs).
+  constexpr int Q = NG / 4;                   // column quads per workgroup tile
+  constexpr int ITEMS = MPAD * Q;             // output quads per workgroup tile
+  constexpr int IPT = (ITEMS + NT - 1) / NT;  // output quads per thread
+  float fws[IPT][4], fbi[IPT][4];
+  auto load_factors = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < IPT; ++it)
+      load_col_factors<1>(a.wscale, a.bias, a.bias_dt, N, grp * NG + ((th + it * NT) / MPAD) * 4,
+                          0, fws[it], fbi[it]);
+  };
+
   // Units: kb_per per split, nkb in total.
   const int u_wg0 = sp * a.kb_per;
   const int u_wg1 = min(a.nkb, u_wg0 + a.kb_per);
@@ -387,8 +402,6 @@ wsp_kernel(const WsArgs a) {
     for (int u = 0; u < NSUB; ++u) red[((wave * MT + t) * NSUB + u) * 64 + lane] = acc[t][u];
   __syncthreads();
 
-  constexpr int Q = NG / 4;        // column quads per workgroup tile
-  constexpr int ITEMS = MPAD * Q;  // output quads per workgroup tile
   auto tile_sum = [&](int item, int &m, int &nl) {
     m = item % MPAD;
     nl = (item / MPAD) * 4;
@@ -400,15 +413,14 @@ wsp_kernel(const WsArgs a) {
     return v;
   };
 
-  auto finish = [&](int m, int n, f32x4 v, float sqsum) {
+  // fw / fb: the factors of columns n .. n + 3
+  auto finish = [&](int m, int n, f32x4 v, float sqsum, const float *fw, const float *fb) {
     const float rs = a.norm ? 1.0f / sqrtf(sqsum / (float)K + a.eps) : 1.0f;
     float o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int nn = min(n + j, N - 1);
-      float t = v[j] * rs;
-      if (a.wscale) t *= a.wscale[nn];
-      if (a.bias) t += load_as_f32(a.bias, a.bias_dt, nn);
+      float t = v[j] * rs * fw[j];
+      if (a.bias) t += fb[j];
       o[j] = t * a.scale;
     }
     const int64_t base = (int64_t)(m0 + m) * N + n;
@@ -428,11 +440,15 @@ wsp_kernel(const WsArgs a) {
   };
 
   if (a.S == 1) {
-    for (int item = th; item < ITEMS; item += NT) {
+    load_factors();
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int item = th + it * NT;
+      if (item >= ITEMS) break;
       int m, nl;
       const f32x4 v = tile_sum(item, m, nl);
       const int n = grp * NG + nl;
-      if (m < Mloc && n < N) finish(m, n, v, sq_row[m]);
+      if (m < Mloc && n < N) finish(m, n, v, sq_row[m], fws[it], fbi[it]);
     }
     return;
   }
@@ -475,7 +491,7 @@ wsp_kernel(const WsArgs a) {
     sq_row[th] = ss;
   }
   __syncthreads();
-  constexpr int IPT = (ITEMS + NT - 1) / NT;  // output quads per thread
+  load_factors();
   f32x4 v[IPT];
 #pragma unroll
   for (int it = 0; it < IPT; ++it) v[it] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -502,7 +518,7 @@ wsp_kernel(const WsArgs a) {
     const int item = th + it * NT;
     const int m = item % MPAD;
     const int n = grp * NG + (item / MPAD) * 4;
-    if (item < ITEMS && m < Mloc && n < N) finish(m, n, v[it], sq_row[m]);
+    if (item < ITEMS && m < Mloc && n < N) finish(m, n, v[it], sq_row[m], fws[it], fbi[it]);
   }
   if (th == 0) ticket_reset(ticket + grp);
 }

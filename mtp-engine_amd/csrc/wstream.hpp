@@ -108,6 +108,48 @@ __device__ __forceinline__ u32x4 bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t o
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past any descriptor's range
+
+// Epilogue factors of the 4 G output columns n0 + gs (i / 4) + i % 4
+// (i < 4 G): wscale[n] (1 without wscale) and bias[n] as fp32 (0 without
+// bias), through buffer descriptors (columns >= N read 0). The dtype choice
+// sits outside the loads so they go out in one batch: issued at the start
+// of a kernel their latency hides behind its main loop, and even at the end
+// they cost one round trip instead of one per element (a load placed
+// between output stores that might alias it waits for its own).
+template <int G>
+__device__ __forceinline__ void load_col_factors(const float *wscale, const void *bias,
+                                                 int bias_dt, int N, int n0, int gs,
+                                                 float (&ws)[4 * G], float (&bi)[4 * G]) {
+  uint32_t off[4 * G];
+#pragma unroll
+  for (int i = 0; i < 4 * G; ++i) {
+    off[i] = (uint32_t)(n0 + gs * (i >> 2) + (i & 3));
+    ws[i] = 1.0f;
+    bi[i] = 0.f;
+  }
+  if (wscale) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(wscale, (uint32_t)N * 4u);
+#pragma unroll
+    for (int i = 0; i < 4 * G; ++i)
+      ws[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off[i] * 4u, 0, 0));
+  }
+  if (bias) {
+    if (bias_dt == MTP_F32) {
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(bias, (uint32_t)N * 4u);
+#pragma unroll
+      for (int i = 0; i < 4 * G; ++i)
+        bi[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off[i] * 4u, 0, 0));
+    } else {
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(bias, (uint32_t)N * 2u);
+      uint32_t h[4 * G];
+#pragma unroll
+      for (int i = 0; i < 4 * G; ++i) h[i] = __builtin_amdgcn_raw_buffer_load_b16(r, off[i] * 2u, 0, 0);
+      const bool bf = bias_dt == MTP_BF16;
+#pragma unroll
+      for (int i = 0; i < 4 * G; ++i) bi[i] = bf ? bf16_bits_to_f32(h[i]) : f16_bits_to_f32(h[i]);
+    }
+  }
+}
 // Cache-policy operand of the buffer intrinsics selecting sc1: the same
 // agent-coherent access the compiler emits for agent-scope atomic loads and
 // stores, here 16 bytes wide (see the hand-off notes in mtp_common.hpp).
@@ -401,18 +443,22 @@ wstream_kernel(const WsArgs a) {
   __syncthreads();
 
   const int Npad = a.G * NG;
+  // epilogue factors of the lane's columns n_wave0 + 16 u + 4 (lane / 16) + j,
+  // in one batch (held through the main loop they would cost registers)
+  float cws[4 * NSUB], cbi[4 * NSUB];
+  load_col_factors<NSUB>(EPI == EPI_LINEAR ? a.wscale : nullptr, a.bias, a.bias_dt, a.N,
+                         n_wave0 + 4 * lg, 16, cws, cbi);
 
   if constexpr (EPI == EPI_LINEAR) {
     // v = columns n .. n+3 of local row m; sqsum = the row's sum of squares.
-    auto finish = [&](int m, int n, f32x4 v, float sqsum) {
+    // fw / fb: the factors of columns n .. n + 3
+    auto finish = [&](int m, int n, f32x4 v, float sqsum, const float *fw, const float *fb) {
       const float rs = a.norm ? 1.0f / sqrtf(sqsum / (float)K + a.eps) : 1.0f;
       float o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int nn = min(n + j, N - 1);
-        float t = v[j] * rs;
-        if (a.wscale) t *= a.wscale[nn];
-        if (a.bias) t += load_as_f32(a.bias, a.bias_dt, nn);
+        float t = v[j] * rs * fw[j];
+        if (a.bias) t += fb[j];
         o[j] = t * a.scale;
       }
       const int64_t base = (int64_t)(m0 + m) * N + n;
@@ -441,7 +487,7 @@ wstream_kernel(const WsArgs a) {
 #pragma unroll
           for (int u = 0; u < NSUB; ++u) {
             const int n = n_wave0 + u * 16 + 4 * lg;
-            if (n < N) finish(m, n, acc[t][u], sqs);
+            if (n < N) finish(m, n, acc[t][u], sqs, cws + 4 * u, cbi + 4 * u);
           }
         }
       }
@@ -476,6 +522,8 @@ wstream_kernel(const WsArgs a) {
       const int m = item / Q;
       const int n = grp * NG + 4 * (item - m * Q);
       if (m >= Mloc || n >= N) continue;
+      float fw[4], fb[4];
+      load_col_factors<1>(a.wscale, a.bias, a.bias_dt, N, n, 0, fw, fb);
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
       float ss = 0.f;
       for (int q = 0; q < a.S; ++q) {
@@ -484,7 +532,7 @@ wstream_kernel(const WsArgs a) {
         for (int j = 0; j < 4; ++j) s[j] += get_f32(src + j);
         ss += get_f32(sqp + ((int64_t)grp * a.S + q) * MPAD + m);
       }
-      finish(m, n, s, ss);
+      finish(m, n, s, ss, fw, fb);
     }
     if (th == 0) ticket_reset(ticket + grp);
   } else {
@@ -501,7 +549,7 @@ wstream_kernel(const WsArgs a) {
             const int n = n_wave0 + u * 16 + 4 * lg + j;
             if (n < N) {
               float v = acc[t][u][j];
-              if (a.bias) v += load_as_f32(a.bias, a.bias_dt, n);
+              if (a.bias) v += cbi[4 * u + j];
               if (argmax_better(v, n, bv, bi)) {
                 bv = v;
                 bi = n;

@@ -117,3 +117,34 @@ def test_int4_workload_full_size():
                         gamma=d["gamma"], norm=True, eps=d["eps"])
     ok, worst = close(y.cpu()[:, cols], ref, RTOL)
     assert ok, f"worst err/bound = {worst:.3g}"
+
+
+def test_int4_leaves_shared_workspace_counters_zero():
+    """INT4 calls and split-K calls share the per-stream workspace: after an
+    INT4 call (its x fragments and scales sit past the counter region) the
+    arrival counters are still zero and a split-K RMSNorm -> linear is exact
+    to the oracle."""
+    import os
+    from mtp_hip import _lib, ops
+    x, packed, scales, gamma = _case(64, 512, 1024, 128, torch.bfloat16, torch.float16, "ref", 3)
+    _run(x, packed, scales, 1024, 128, "ref", gamma, True)
+    ws = _lib._workspaces[(0, torch.cuda.current_stream().cuda_stream)]
+    counters = ws[:65536]  # MTP_WORKSPACE_COUNTER_BYTES (include/mtp_hip.h)
+    assert int(counters.count_nonzero()) == 0
+    g = torch.Generator().manual_seed(11)
+    xl = torch.randn(33, 1024, generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(260, 1024, generator=g)).to(torch.bfloat16)
+    gm = 1 + 0.1 * torch.randn(1024, generator=g)
+    old = os.environ.get("MTP_SK_SPLITS")
+    os.environ["MTP_SK_SPLITS"] = "3"
+    try:
+        y = ops.rmsnorm_linear(xl.to(DEV), W.to(DEV), None, 1e-6, 1.0, gamma=gm.to(DEV))
+    finally:
+        if old is None:
+            os.environ.pop("MTP_SK_SPLITS", None)
+        else:
+            os.environ["MTP_SK_SPLITS"] = old
+    torch.cuda.synchronize()
+    ok, worst = close(y, O.rmsnorm_linear(xl, W, None, 1e-6, 1.0, gamma=gm), 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+    assert int(counters.count_nonzero()) == 0
