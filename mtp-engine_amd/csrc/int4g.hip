@@ -3,10 +3,16 @@
 
 namespace mtp {
 
-I4Kernel int4_gemm_pick(int mt, int na) {
-  if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1>;
-  if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1>;
-  if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2>;
+I4Kernel int4_gemm_pick(int mt, int na, int nw) {
+  if (nw == 4) {
+    if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1, 4>;
+    if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1, 4>;
+    if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2, 4>;
+  } else if (nw == 8) {
+    if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1, 8>;
+    if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1, 8>;
+    if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2, 8>;
+  }
   return nullptr;
 }
 

@@ -217,9 +217,13 @@ __device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned ch
 #endif
 }
 
-template <int MT, int NA>
-__global__ void __launch_bounds__(256, 1)
+template <int MT, int NA, int NWV>
+__global__ void __launch_bounds__(64 * NWV, 1)
 int4_gemm_kernel(const I4Args a) {
+  // NWV = 8: waves split each unit's k-steps in halves (wave = row quarter
+  // + 4 k-half), two waves per SIMD; the halves' sums meet in LDS at the end
+  constexpr bool KH = NWV == 8;
+  constexpr int KSW = KH ? 4 : 8;         // k-steps per wave per unit
   constexpr int BN = 128 * NA, UK = 128;
   constexpr int TILE = 8 * 1024;          // bytes of one 32-row x tile per unit
   constexpr int XST = MT * TILE;          // x bytes of one LDS stage
@@ -227,8 +231,12 @@ int4_gemm_kernel(const I4Args a) {
   constexpr int SST = 4 * 1024;           // scale bytes of one LDS stage (4 runs of 32 k)
   constexpr int STAGE = XST + WST + SST;
   constexpr int NS = 3;                   // LDS stages (copies run two units ahead)
-  constexpr int ND = 2 * MT;              // x copies per wave per unit
-  constexpr int NWL = BN / 64;            // weight copies per wave per unit (16 rows each)
+  constexpr int ND = 8 * MT / NWV;        // x copies per wave per unit
+  constexpr int NWL = BN / 16 / NWV;      // weight copies per wave per unit (16 rows each)
+  static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
+  static_assert((8 * MT) % NWV == 0 && (BN / 16) % NWV == 0, "copies divide among the waves");
+  static_assert(!KH || NA * MT * 16 * 1024 <= 3 * (MT * 8 * 1024 + BN * 64 + 4 * 1024),
+                "k-half merge fits the LDS stages");
   constexpr int NV = NWL + 1 + ND;        // vector-memory instructions per wave per unit
   __shared__ __attribute__((aligned(1024))) unsigned char xs[NS * STAGE];
 
@@ -238,6 +246,8 @@ int4_gemm_kernel(const I4Args a) {
   // offset (which depends on it) in scalar registers, without a waterfall
   const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
   const int h = lane >> 5, l32 = lane & 31;
+  const int rq = KH ? wave & 3 : wave;  // row quarter: A tiles NA rq .. NA rq + NA - 1
+  const int kh = KH ? wave >> 2 : 0;    // k-half (k-steps 4 kh .. 4 kh + 3)
 
   // blockIdx -> (column group, row group): the row groups of column group
   // c are workgroups with b % 8 == c % 8 (one XCD).
@@ -265,9 +275,10 @@ int4_gemm_kernel(const I4Args a) {
   const int nunits = a.K / UK;
 
   // Weights: per unit the workgroup's BN rows x 64 bytes are copied to LDS
-  // row-major, 16 rows x 64 bytes per copy (copy c = wave + 4 i; lane L
+  // row-major, 16 rows x 64 bytes per copy (copy c = wave + NWV i; lane L
   // takes bytes 16 (L % 4) .. + 15 of row 16 c + L / 4). The MFMA A operand
-  // of subtile t is read back per lane: row wcol[t], bytes 32 h .. + 31.
+  // of subtile t is read back per lane: row wcol[t], bytes 32 h .. + 31 (16
+  // of them per k-half).
   const uint32_t ldw = (uint32_t)a.K / 2;
   const int nrows = min(BN, a.N - n0);
   const __amdgpu_buffer_rsrc_t wrs =
@@ -275,28 +286,34 @@ int4_gemm_kernel(const I4Args a) {
   uint32_t wvo[NWL];
 #pragma unroll
   for (int i = 0; i < NWL; ++i)
-    wvo[i] = (uint32_t)(16 * (wave + 4 * i) + (lane >> 2)) * ldw + 16u * (lane & 3);
+    wvo[i] = (uint32_t)(16 * (wave + NWV * i) + (lane >> 2)) * ldw + 16u * (lane & 3);
   int wcol[NA];  // row of the lane inside the workgroup's BN
 #pragma unroll
-  for (int t = 0; t < NA; ++t) wcol[t] = 32 * (NA * wave + t) + l32;
+  for (int t = 0; t < NA; ++t) wcol[t] = 32 * (NA * rq + t) + l32;
   // fp16 scales, transposed: scale of row n, group g at scT[g * ldst + n].
-  // Per unit, wave w copies the scales of k-run w (k = 128 u + 32 w .. + 31)
-  // for the BN rows: lanes 0 .. BN / 8 - 1 copy 16 bytes each, the others
-  // read past the descriptor into an unused part of the LDS row.
+  // Per unit the scales of the 4 k-runs (k = 128 u + 32 r .. + 31) for the
+  // BN rows go to LDS run by run (1 KB each, BN * 2 bytes used). 4 waves:
+  // wave w copies run w, lanes 0 .. BN / 8 - 1 16 bytes each, the others
+  // read past the descriptor into the unused part of the run. 8 waves: wave
+  // w copies half w / 4 (rows BN / 2 * (w / 4) ..) of run w % 4 with lanes
+  // 0 .. BN / 16 - 1 only (the other lanes are masked off: their zeros would
+  // land on the other half).
   const __amdgpu_buffer_rsrc_t srs =
       make_rsrc((const uint16_t *)a.scales + n0, (uint32_t)(a.ng * a.ldst - n0) * 2u);
-  const uint32_t svo = lane < BN / 8 ? (uint32_t)lane * 16u : kOOB;
+  const int srun = KH ? wave & 3 : wave;
+  const uint32_t shalf = KH ? (uint32_t)(wave >> 2) * BN : 0u;  // bytes
+  const uint32_t svo = lane < BN / 8 ? (uint32_t)lane * 16u + shalf : kOOB;
   const uint32_t ldst2 = (uint32_t)a.ldst * 2u;
   // x tiles of this workgroup: MT consecutive 32-row tiles of the
   // fragment-major copy; tile T, unit u starts at byte (T * U + u) * TILE.
   const unsigned char *xbase = (const unsigned char *)a.xn + (int64_t)rg * MT * nunits * TILE;
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(xbase, (uint32_t)(MT * nunits) * TILE);
-  // x copy c of a unit (c = wave + 4 i): tile c / 8, k-step c % 8; the
+  // x copy c of a unit (c = wave + NWV i): tile c / 8, k-step c % 8; the
   // unit goes in the scalar offset, the per-lane part is fixed.
   uint32_t xvo[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i) {
-    const int c = wave + 4 * i;
+    const int c = wave + NWV * i;
     xvo[i] = (uint32_t)((c >> 3) * nunits * TILE + (c & 7) * 1024 + lane * 16);
   }
 
@@ -310,16 +327,20 @@ int4_gemm_kernel(const I4Args a) {
     const bool live = unit < nunits;
     const int su = live ? unit : 0;
     if constexpr (v < NWL) {
-      lds_copy16(wrs, xs + slot * STAGE + XST + (wave + 4 * v) * 1024, live ? wvo[v] : kOOB,
+      lds_copy16(wrs, xs + slot * STAGE + XST + (wave + NWV * v) * 1024, live ? wvo[v] : kOOB,
                  su * 64);
     } else if constexpr (v == NWL) {
-      const int k = su * UK + 32 * wave;
+      const int k = su * UK + 32 * srun;
       const int g = a.glog >= 0 ? k >> a.glog : k / a.group;
-      lds_copy16(srs, xs + slot * STAGE + XST + WST + wave * 1024, live ? svo : kOOB,
-                 (int)((uint32_t)g * ldst2));
+      unsigned char *dst = xs + slot * STAGE + XST + WST + srun * 1024 + shalf;
+      if constexpr (KH) {
+        if (lane < BN / 16) lds_copy16(srs, dst, live ? svo : kOOB, (int)((uint32_t)g * ldst2));
+      } else {
+        lds_copy16(srs, dst, live ? svo : kOOB, (int)((uint32_t)g * ldst2));
+      }
     } else {
       const int i = v - NWL - 1;
-      const int c = wave + 4 * i;
+      const int c = wave + NWV * i;
       lds_copy16(xrs, xs + slot * STAGE + (c >> 3) * TILE + (c & 7) * 1024, live ? xvo[i] : kOOB,
                  su * TILE);
     }
@@ -345,25 +366,30 @@ int4_gemm_kernel(const I4Args a) {
     const unsigned char *sx = xs + slot * STAGE + lane * 16;
     const unsigned char *sw = xs + slot * STAGE + XST;
     const unsigned char *ss = xs + slot * STAGE + XST + WST;
-    u32x4 wr[NA][2];
+    // the wave's 16-byte halves of its A rows (both, or its k-half's) and
+    // the scales of their 32-k runs
+    constexpr int NE = KH ? 1 : 2;
+    u32x4 wr[NA][NE];
 #pragma unroll
     for (int t = 0; t < NA; ++t)
 #pragma unroll
-      for (int e = 0; e < 2; ++e) wr[t][e] = *(const u32x4 *)(sw + wcol[t] * 64 + 32 * h + 16 * e);
-    h2 s2[NA][2];
+      for (int e = 0; e < NE; ++e)
+        wr[t][e] = *(const u32x4 *)(sw + wcol[t] * 64 + 32 * h + 16 * (KH ? kh : e));
+    h2 s2[NA][NE];
 #pragma unroll
     for (int t = 0; t < NA; ++t)
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const _Float16 f = *(const _Float16 *)(ss + (2 * h + g) * 1024 + wcol[t] * 2);
+      for (int g = 0; g < NE; ++g) {
+        const _Float16 f = *(const _Float16 *)(ss + (2 * h + (KH ? kh : g)) * 1024 + wcol[t] * 2);
         s2[t][g] = h2{f, f};
       }
+    // wave k-step s (0 .. KSW - 1) is k-step 4 kh + s of the unit
     auto decode = [&](h8 (&af)[NA], int s) __attribute__((always_inline)) {
 #pragma unroll
       for (int t = 0; t < NA; ++t) {
-        const uint32_t w = wr[t][s >> 2][s & 3] ^ flip;
+        const uint32_t w = wr[t][KH ? 0 : s >> 2][s & 3] ^ flip;
         const uint32_t w8 = w >> 8;
-        const h2 sv = s2[t][s >> 2];
+        const h2 sv = s2[t][KH ? 0 : s >> 2];
         const uint32_t q0 = (w & 0x000F000Fu) | 0x64006400u;
         const uint32_t q1 = (w & 0x00F000F0u) | 0x64006400u;
         const uint32_t q2 = (w8 & 0x000F000Fu) | 0x64006400u;
@@ -378,15 +404,15 @@ int4_gemm_kernel(const I4Args a) {
     };
     auto read_b = [&](h8 (&bv)[MT], int s) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < MT; ++j) bv[j] = *(const h8 *)(sx + j * TILE + s * 1024);
+      for (int j = 0; j < MT; ++j) bv[j] = *(const h8 *)(sx + j * TILE + (4 * kh + s) * 1024);
     };
     h8 af[2][NA], bv[2][MT];
     read_b(bv[0], 0);
     decode(af[0], 0);
-    static_for<0, 8>([&](auto sc_) {
+    static_for<0, KSW>([&](auto sc_) {
       constexpr int s = decltype(sc_)::value;
-      static_for<s * NV / 8, (s + 1) * NV / 8>([&](auto vc) { issue(vc, nunit, nslot); });
-      if constexpr (s + 1 < 8) {
+      static_for<s * NV / KSW, (s + 1) * NV / KSW>([&](auto vc) { issue(vc, nunit, nslot); });
+      if constexpr (s + 1 < KSW) {
         read_b(bv[(s + 1) & 1], s + 1);
         decode(af[(s + 1) & 1], s + 1);
       }
@@ -431,8 +457,23 @@ int4_gemm_kernel(const I4Args a) {
   // no copy into LDS may still be in flight when the workgroup ends
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // epilogue: acc[t][j][e] = y[m][n] with m = m0 + 32 j + l32 and
-  // n = n0 + wcol[t] - l32 + 8 (e / 4) + 4 h + e % 4.
+  // k-halves: the waves of half 1 hand their sums to those of half 0
+  // through LDS (the stages are free now), [rq][t][j][lane]
+  f32x16 *red = (f32x16 *)xs;
+  if constexpr (KH) {
+    __syncthreads();
+    if (kh == 1) {
+#pragma unroll
+      for (int t = 0; t < NA; ++t)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) red[((rq * NA + t) * MT + j) * 64 + lane] = acc[t][j];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+  }
+
+  // epilogue: acc[t][j][e] (plus the other k-half's red entry) = y[m][n]
+  // with m = m0 + 32 j + l32 and n = n0 + wcol[t] - l32 + 8 (e / 4) + 4 h + e % 4.
   const int m0 = rg * MT * 32;
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
@@ -445,8 +486,14 @@ int4_gemm_kernel(const I4Args a) {
       for (int g = 0; g < 4; ++g) {
         const int n = n0 + wcol[t] - l32 + 8 * g + 4 * h;
         const int64_t base = (int64_t)m * a.N + n;
-        const float v0 = acc[t][j][4 * g] * om, v1 = acc[t][j][4 * g + 1] * om;
-        const float v2 = acc[t][j][4 * g + 2] * om, v3 = acc[t][j][4 * g + 3] * om;
+        float r4[4] = {acc[t][j][4 * g], acc[t][j][4 * g + 1], acc[t][j][4 * g + 2],
+                       acc[t][j][4 * g + 3]};
+        if constexpr (KH) {
+          const f32x4 o = ((const f32x4 *)&red[((rq * NA + t) * MT + j) * 64 + lane])[g];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r4[e] += o[e];
+        }
+        const float v0 = r4[0] * om, v1 = r4[1] * om, v2 = r4[2] * om, v3 = r4[3] * om;
         if (n + 3 < a.N && a.yvec) {
           uint2 pk;
           if (a.ydt == MTP_BF16) {

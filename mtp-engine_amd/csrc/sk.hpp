@@ -28,8 +28,9 @@
 //     of W goes from registers to LDS (double-buffered), where each wave
 //     reads the A operands of its k-steps. One barrier per stage.
 //     W sits in LDS row-major with 16-byte chunk c of row r at position
-//     c ^ (r % 8) (the A-operand reads of 32 consecutive rows then hit
-//     distinct banks); for fp8 the A operand is upcast exactly in registers.
+//     c ^ sk_swz(r) (the A-operand reads of 16 consecutive rows then hit
+//     distinct bank groups); for fp8 the A operand is upcast exactly in
+//     registers.
 //     k-slot order: within 32 k of a stage (two k-steps for fp8), lane group
 //     g = lane / 32 holds k 16 g .. 16 g + 15, the first 8 in k-step 2p, the
 //     other 8 in k-step 2p + 1 (16-bit W: k-step j, lane group g holds
@@ -64,6 +65,18 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
+
+// LDS position of 16-byte chunk c of W row r inside the row's 128 bytes is
+// c ^ sk_swz(r): the A-operand reads of 16 consecutive rows (rows r and r + 8
+// are 1 KB apart, the same banks) then hit 16 distinct bank groups.
+__device__ __forceinline__ int sk_swz(int r) { return (r >> 1) & 7; }
+// Kernels that stage raw x rows into B-operand blocks (1 KB per k-step j and
+// 32-row tile, lane L = 32 g + row % 32 holding 8 k of lane group g) put
+// lane L at slot L ^ sk_xswz(j, g): the stores of one 8-rows x 128-byte load
+// (two rows x 8 chunks per 16 lanes, every chunk a different (j % 4, g))
+// then hit 16 distinct bank groups, and the B reads stay a permutation
+// within each 16-lane group.
+__device__ __forceinline__ int sk_xswz(int j, int g) { return 4 * (j & 3) + 2 * g; }
 
 // (k-step, lane group) of 16-byte chunk q (8 k) of a stage.
 template <bool FP8>
@@ -201,7 +214,7 @@ sk_kernel(const SkArgs a) {
 #pragma unroll
   for (int i = 0; i < NWC; ++i) {
     const int row = 8 * (wave + 4 * i) + (lane >> 3);
-    const int chunk = (lane & 7) ^ (row & 7);
+    const int chunk = (lane & 7) ^ sk_swz(row);
     wvo[i] = (uint32_t)row * ldw + (uint32_t)st0 * kSkUB + 16u * chunk;
   }
   // xn load i = t * KPW + jj of the wave: tile t, k-step wave * KPW + jj
@@ -225,7 +238,7 @@ sk_kernel(const SkArgs a) {
   // access (the scalar offset is not part of the descriptor's range check),
   // into a slot that is never computed on, so the count of instructions per
   // stage is always NV.
-  auto issue = [&](auto vc, int st, auto slotc) {
+  auto issue = [&](auto vc, int st, auto slotc) __attribute__((always_inline)) {
     constexpr int v = decltype(vc)::value, slot = decltype(slotc)::value;
     const bool live = st < nst;
     const int str = live ? (st + rot < nst ? st + rot : st + rot - nst) : 0;
@@ -252,13 +265,13 @@ sk_kernel(const SkArgs a) {
   // the xn blocks), with the copies of stage `nst_` spread over them.
   const int ag = lane >> 5;
   // W of ring slot `slot` to LDS buffer b
-  auto w_to_lds = [&](auto slotc, int b) {
+  auto w_to_lds = [&](auto slotc, int b) __attribute__((always_inline)) {
     constexpr int slot = decltype(slotc)::value;
 #pragma unroll
     for (int v = 0; v < NWC; ++v)
       *(u32x4 *)(lds + b * STAGE + (wave + 4 * v) * 1024 + lane * 16) = wr[slot][v];
   };
-  auto compute = [&](auto slotc, int nst_, auto nslotc) {
+  auto compute = [&](auto slotc, int nst_, auto nslotc) __attribute__((always_inline)) {
     constexpr int slot = decltype(slotc)::value;
     const unsigned char *base = lds + (slot & 1) * STAGE;
     static_for<0, KPW>([&](auto jc) {
@@ -272,7 +285,7 @@ sk_kernel(const SkArgs a) {
         if constexpr (FP8) {
           // chunk 2 (j / 2) + g holds k-steps j (bytes 0..7) and j + 1 (8..15)
           const int c = 2 * (j >> 1) + ag;
-          const u32x4 w = *(const u32x4 *)(base + row * kSkUB + ((c ^ (row & 7)) << 4));
+          const u32x4 w = *(const u32x4 *)(base + row * kSkUB + ((c ^ sk_swz(row)) << 4));
           const int h = (j & 1) * 2;
           av[u][0] = fp8x2_to_ct<CT, false>(w[h]);
           av[u][1] = fp8x2_to_ct<CT, true>(w[h]);
@@ -280,7 +293,7 @@ sk_kernel(const SkArgs a) {
           av[u][3] = fp8x2_to_ct<CT, true>(w[h + 1]);
         } else {
           const int c = 2 * j + ag;
-          av[u] = *(const u32x4 *)(base + row * kSkUB + ((c ^ (row & 7)) << 4));
+          av[u] = *(const u32x4 *)(base + row * kSkUB + ((c ^ sk_swz(row)) << 4));
         }
       }
 #pragma unroll
@@ -305,7 +318,7 @@ sk_kernel(const SkArgs a) {
   });
   w_to_lds(std::integral_constant<int, 0>{}, 0);
   lds_barrier();
-  auto step = [&](auto rc, int s) {
+  auto step = [&](auto rc, int s) __attribute__((always_inline)) {
     constexpr int r = decltype(rc)::value;  // s % NS
     __builtin_amdgcn_sched_barrier(0);
     // W of stage s + 1 to the other LDS buffer (the barrier below publishes

@@ -19,7 +19,7 @@
 // 16-bit W) and the matching x. Per stage:
 //   * W comes HBM -> registers with 8-rows x 128-byte non-temporal loads
 //     NS - 1 stages ahead, then goes to a double-buffered LDS stage (16-byte
-//     chunk c of row r at c ^ skl_swz(r)) one step before use;
+//     chunk c of row r at c ^ sk_swz(r)) one step before use;
 //   * x comes from the caller's row-major rows with the same 8-rows x
 //     128-byte loads; on its way to LDS each lane adds the squares of its
 //     8 values to the row's sum and multiplies them by gamma (staged in LDS
@@ -49,16 +49,6 @@
 
 namespace mtp {
 
-// LDS position of 16-byte chunk c of W row r inside the row's 128 bytes is
-// c ^ skl_swz(r): the A-operand reads of 16 consecutive rows (8 bank groups
-// per row pair apart) then hit 16 distinct bank groups.
-__device__ __forceinline__ int skl_swz(int r) { return (r >> 1) & 7; }
-// Slot of B-operand lane L in its 1 KB block (k-step j, lane group g = L /
-// 32) is L ^ skl_xswz(j, g): the x staging stores of one load instruction
-// (two rows x 8 chunks per 16 lanes, every chunk a different (j % 4, g))
-// then hit 16 distinct bank groups, and the B reads stay a permutation
-// within each 16-lane group.
-__device__ __forceinline__ int skl_xswz(int j, int g) { return 4 * (j & 3) + 2 * g; }
 
 template <int CT, int WT, int MT, int NW, bool GAM>
 __global__ void __launch_bounds__(64 * NW, 1)
@@ -113,7 +103,7 @@ skl_kernel(const SklArgs a) {
 #pragma unroll
   for (int i = 0; i < NWC; ++i) {
     const int row = 8 * (wave + NW * i) + (lane >> 3);
-    const int chunk = (lane & 7) ^ skl_swz(row);
+    const int chunk = (lane & 7) ^ sk_swz(row);
     wvo[i] = (uint32_t)row * ldw + 16u * chunk;
   }
   // x load c (c = wave + NW i, c < NXL): rows 8 (c % 4 MT) + l / 8 (rows
@@ -138,7 +128,7 @@ skl_kernel(const SklArgs a) {
       int j, g;
       sk_chunk_slot<FP8>(q, j, g);
       xvo[i] = (uint32_t)row * ldx + 16u * (uint32_t)q;
-      xl[i] = (((row >> 5) * KS + j) * 64 + ((32 * g + (row & 31)) ^ skl_xswz(j, g))) * 16;
+      xl[i] = (((row >> 5) * KS + j) * 64 + ((32 * g + (row & 31)) ^ sk_xswz(j, g))) * 16;
       xq[i] = q;
     }
   }
@@ -228,7 +218,7 @@ skl_kernel(const SklArgs a) {
       if constexpr (FP8) {
         if constexpr ((j & 1) == 0) {
           const int c = j + ag;  // chunk 2 (j / 2) + g: k-steps j and j + 1
-          wq = *(const u32x4 *)(wb + row * kSkUB + ((c ^ skl_swz(row)) << 4));
+          wq = *(const u32x4 *)(wb + row * kSkUB + ((c ^ sk_swz(row)) << 4));
         }
         constexpr int h = (j & 1) * 2;
         av[0] = fp8x2_to_ct<CT, false>(wq[h]);
@@ -237,12 +227,12 @@ skl_kernel(const SklArgs a) {
         av[3] = fp8x2_to_ct<CT, true>(wq[h + 1]);
       } else {
         const int c = 2 * j + ag;
-        av = *(const u32x4 *)(wb + row * kSkUB + ((c ^ skl_swz(row)) << 4));
+        av = *(const u32x4 *)(wb + row * kSkUB + ((c ^ sk_swz(row)) << 4));
       }
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         const u32x4 bv =
-            *(const u32x4 *)(xb + (t * KS + j) * 1024 + ((lane ^ skl_xswz(j, ag)) << 4));
+            *(const u32x4 *)(xb + (t * KS + j) * 1024 + ((lane ^ sk_xswz(j, ag)) << 4));
         acc[t] = mfma32<CT>(av, bv, acc[t]);
       }
     });

@@ -14,7 +14,7 @@
 // no reduction between waves. Per stage:
 //   * W (256 rows x 128 bytes) comes HBM -> registers with 8-rows x 128-byte
 //     non-temporal loads NS - 1 stages ahead, then goes to a double-buffered
-//     LDS stage (16-byte chunk c of row r at c ^ (r % 8)) one step before use;
+//     LDS stage (16-byte chunk c of row r at c ^ sk_swz(r)) one step before use;
 //   * x comes from the caller's row-major hidden rows with the same
 //     8-rows x 128-byte loads (one per wave per stage), each lane storing
 //     its 16 bytes into LDS at their place in the B-operand blocks of the
@@ -80,12 +80,12 @@ skv_kernel(const SkvArgs a) {
   const uint32_t ldw = (uint32_t)K * 2u;
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)N * ldw);
   // W load c (c = wave + 8 i): rows 8 c .. 8 c + 7 of the tile, lane l: row
-  // 8 c + l / 8, 16-byte chunk (l % 8) ^ (row % 8) of the stage's 128 bytes
+  // 8 c + l / 8, 16-byte chunk (l % 8) ^ sk_swz(row) of the stage's 128 bytes
   uint32_t wvo[NWC];
 #pragma unroll
   for (int i = 0; i < NWC; ++i) {
     const int row = 8 * (wave + 8 * i) + (lane >> 3);
-    const int chunk = (lane & 7) ^ (row & 7);
+    const int chunk = (lane & 7) ^ sk_swz(row);
     wvo[i] = (uint32_t)row * ldw + 16u * chunk;
   }
   // x load of wave w (w < 4 MT): rows 8 w .. 8 w + 7 (rows past M read as
@@ -95,7 +95,8 @@ skv_kernel(const SkvArgs a) {
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)a.M * ldw);
   const int xrow = 8 * wave + (lane >> 3), xc = lane & 7;
   const uint32_t xvo = (uint32_t)xrow * ldw + 16u * (uint32_t)xc;
-  const int xlds = ((xrow >> 5) * KS + (xc >> 1)) * 1024 + (32 * (xc & 1) + (xrow & 31)) * 16;
+  const int xlds = ((xrow >> 5) * KS + (xc >> 1)) * 1024 +
+                   ((32 * (xc & 1) + (xrow & 31)) ^ sk_xswz(xc >> 1, xc & 1)) * 16;
   u32x4 wr[NS][NWC];  // W register ring
   u32x4 xr[NS];       // x register ring
 
@@ -152,10 +153,11 @@ skv_kernel(const SkvArgs a) {
       constexpr int j = decltype(jc)::value;
       static_for<j * NV / KS, (j + 1) * NV / KS>([&](auto vc) { issue(vc, nslotc); });
       const int c = 2 * j + ag;
-      const u32x4 av = *(const u32x4 *)(wb + row * kSkUB + ((c ^ (row & 7)) << 4));
+      const u32x4 av = *(const u32x4 *)(wb + row * kSkUB + ((c ^ sk_swz(row)) << 4));
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const u32x4 bv = *(const u32x4 *)(xb + (t * KS + j) * 1024 + lane * 16);
+        const u32x4 bv =
+            *(const u32x4 *)(xb + (t * KS + j) * 1024 + ((lane ^ sk_xswz(j, ag)) << 4));
         acc[t] = mfma32<CT>(av, bv, acc[t]);
       }
     });
