@@ -119,9 +119,65 @@ __device__ __forceinline__ void transpose_scales_t(const void *__restrict__ scal
     }
   }
 }
+// The same with one 16-byte load per lane (EPC groups of one row) when the
+// rows are whole 16-byte chunks: lane n of a wave takes row n0 + n, the
+// waves take the chunks in turn, and every store of a wave writes 64
+// consecutive rows of one group (128 contiguous bytes).
+template <int SDT>
+__device__ __forceinline__ void transpose_scales_v(const void *__restrict__ scales, int64_t N,
+                                                   int64_t ng, int64_t ldst, int64_t n0,
+                                                   uint16_t *__restrict__ scT) {
+  constexpr int EPC = SDT == MTP_F32 ? 4 : 8;  // groups per 16-byte chunk
+  const int64_t nch = ng / EPC;
+  const int64_t n = n0 + (threadIdx.x & 63);
+  if (n >= N) return;
+  // the whole [N, ng] matrix through one descriptor (< 2 GiB: the host
+  // limits ng * ldst * 2); chunks past the row load with an out-of-range
+  // offset (zeros, never stored)
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(N * nch * 16));
+  for (int64_t c0 = threadIdx.x >> 6; c0 < nch; c0 += 4 * 4) {
+    u32x4 raw[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = c0 + 4 * u;
+      raw[u] = bload16(rs, c < nch ? (uint32_t)((n * nch + c) * 16) : kOOB);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = c0 + 4 * u;
+      if (c >= nch) break;
+      float f[EPC];
+      if constexpr (SDT == MTP_F32) {
+        const f32x4 v = __builtin_bit_cast(f32x4, raw[u]);
+        f[0] = v[0];
+        f[1] = v[1];
+        f[2] = v[2];
+        f[3] = v[3];
+      } else {
+        const uint32_t d[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t h = (e & 1) ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu;
+          f[e] = SDT == MTP_BF16 ? __builtin_bit_cast(float, h << 16)
+                                 : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; ++e)
+        scT[(c * EPC + e) * ldst + n] = __builtin_bit_cast(uint16_t, (_Float16)f[e]);
+    }
+  }
+}
 __device__ __forceinline__ void transpose_scales(const void *scales, int sdt, int64_t N,
                                                  int64_t ng, int64_t ldst, int64_t n0,
                                                  uint16_t *scT) {
+  const int epc = sdt == MTP_F32 ? 4 : 8;
+  if ((((uintptr_t)scales) & 15) == 0 && ng % epc == 0) {
+    if (sdt == MTP_F32) transpose_scales_v<MTP_F32>(scales, N, ng, ldst, n0, scT);
+    else if (sdt == MTP_BF16) transpose_scales_v<MTP_BF16>(scales, N, ng, ldst, n0, scT);
+    else transpose_scales_v<MTP_F16>(scales, N, ng, ldst, n0, scT);
+    return;
+  }
   if (sdt == MTP_F32) transpose_scales_t<MTP_F32>(scales, N, ng, ldst, n0, scT);
   else if (sdt == MTP_BF16) transpose_scales_t<MTP_BF16>(scales, N, ng, ldst, n0, scT);
   else transpose_scales_t<MTP_F16>(scales, N, ng, ldst, n0, scT);
