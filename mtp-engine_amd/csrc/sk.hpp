@@ -204,7 +204,7 @@ sk_kernel(const SkArgs a) {
 
   // W load c (c = wave + 4 i): rows 8 c .. 8 c + 7, lane l: row 8 c + l / 8;
   // the LDS write of a load is 64 lanes x 16 bytes contiguous, so the
-  // swizzle (chunk c' of the row at position c' ^ (row % 8)) is in the chunk
+  // swizzle (chunk c' of the row at position c' ^ sk_swz(row)) is in the chunk
   // a lane fetches
   const uint32_t ldw = (uint32_t)K * (FP8 ? 1u : 2u);
   const int nrows = min(kSkBN, N - n0);

@@ -94,7 +94,7 @@ skl_kernel(const SklArgs a) {
   };
 
   // W load c (c = wave + NW i): rows 8 c .. 8 c + 7 of the tile, lane l: row
-  // 8 c + l / 8, 16-byte chunk (l % 8) ^ (row % 8) of the stage's 128 bytes
+  // 8 c + l / 8, 16-byte chunk (l % 8) ^ sk_swz(row) of the stage's 128 bytes
   const uint32_t ldw = (uint32_t)K * (FP8 ? 1u : 2u);
   const int nrows = min(BN, N - n0);
   const __amdgpu_buffer_rsrc_t wrs =
