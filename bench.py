@@ -278,8 +278,9 @@ def cpu_baseline_fp8(torch, M: int):
                                       gamma=d["gamma"])
     fn()
     times = []
+    # a bounded sample: repeated full calls for about 10 s of CPU work
     t_end = time.time() + 10.0
-    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+    while len(times) < 5 or (time.time() < t_end and len(times) < 2000):
         t = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t)
