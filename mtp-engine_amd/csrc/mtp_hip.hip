@@ -413,13 +413,16 @@ struct PlanSkl {
 constexpr int kSklCUs = 256;  // compute units of the device (one workgroup each)
 
 // MTP_SKL=1 forces the single-launch kernel wherever it applies, MTP_SKL=0
-// turns it off; by default it runs where its 256-column tiles fill the CUs
-// without a K-split (N > 128 * 256): a split's hand-off through the device
-// coherence point (partial stores, arrival ticket, partial loads) costs
-// about 7 us at the end of the launch, more than the x traffic it saves.
-// Measured, fp8 W, K 4096: M 64 N 131072 144 us vs 174 us (tiled 64-column
-// kernel), M 16 N 131072 95 us vs 153 us; M 64 N 14336 (four splits) 27.8
-// us vs 25.7 us.
+// turns it off. By default it runs where its 256-column tiles fill the CUs
+// without a K-split (N > 128 * 256), and for at most 16 rows once W is large
+// enough (>= 48 MiB) to repay a split's hand-off through the device
+// coherence point (partial stores, arrival ticket, partial loads: about
+// 7 us at the end of the launch). Measured, K 4096: fp8 M 64 N 131072 144
+// us vs 174 us (64-column kernel), M 16 N 131072 95 us vs 153 us; with
+// splits, fp8 M 8 N 28672 27.9 us vs 37.1 us (row-chunk kernel), M 16 N
+// 14336 18.6 vs 21.5, M 8 N 8192 17.8 vs 14.5 (below the bound), bf16 M 16
+// N 28672 51.4 vs 72.1; fp8 M 64 N 14336 (four splits) 27.8 us vs 25.7 us.
+constexpr int64_t kSklSplitMinWBytes = (int64_t)48 << 20;
 int skl_mode() {
   const char *e = std::getenv("MTP_SKL");
   if (!e || !*e) return -1;
@@ -535,7 +538,9 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   const int sklm = skl_mode();
   if (sklm != 0) {
     const PlanSkl pl = make_plan_skl(xt, wt, M, N, K, gamma != nullptr);
-    if (pl.ok && (sklm == 1 || pl.S == 1) && aligned && (!gamma || gt == MTP_F32)) {
+    const bool wide = pl.S == 1;
+    const bool big_skinny = M <= 16 && N * K * dtype_bytes(wt) >= kSklSplitMinWBytes;
+    if (pl.ok && (sklm == 1 || wide || big_skinny) && aligned && (!gamma || gt == MTP_F32)) {
       if (!ws || ws_bytes < pl.total) return MTP_ERR_WORKSPACE;
       SklArgs la{};
       la.x = x;

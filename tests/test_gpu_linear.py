@@ -233,6 +233,29 @@ def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
     assert torch.equal(y, y3)
 
 
+@pytest.mark.parametrize("M,N,K,wkind", [(3, 8192, 4096, "same"), (13, 12288, 4096, "fp8")])
+def test_single_launch_default_route_few_rows(M, N, K, wkind):
+    """At most 16 rows with at least 48 MiB of W take the single-launch
+    kernel with K-splits by default (no environment override)."""
+    from mtp_hip import ops
+    print(f"case skl default few rows M={M} N={N} K={K} w={wkind}", flush=True)
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), None, 1e-6, gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, None, 1e-6, gamma=gm)
+    else:
+        Wc = W.to(torch.bfloat16)
+        y = ops.rmsnorm_linear(_dev(x), _dev(Wc), None, 1e-6, 1.0, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, None, 1e-6, 1.0, gamma=gm)
+    torch.cuda.synchronize()
+    ok, worst = close(y, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
 @pytest.mark.parametrize("M", [8, 32, 64])
 def test_fp8_workload_full_size(M):
     """The fp8-e4m3 RMSNorm+linear workload: x bf16 [M,4096], W [14336,4096]."""
