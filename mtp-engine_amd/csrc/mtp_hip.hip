@@ -538,8 +538,16 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   const int sklm = skl_mode();
   if (sklm != 0) {
     const PlanSkl pl = make_plan_skl(xt, wt, M, N, K, gamma != nullptr);
+    // with splits: <= 16 rows from 48 MiB of W; fp8 W also 17 .. 32 rows
+    // from 48 MiB and 33 .. 64 rows from 96 MiB (fp8 K 4096: M 24 N 14336
+    // 18.7 us vs 20.4, M 64 N 28672 37.5 vs 44.6, M 64 N 14336 27.8 vs 25.0;
+    // 16-bit W above 16 rows ties or loses: M 32 N 8192 K 8192 35.0 vs 31.9)
     const bool wide = pl.S == 1;
-    const bool big_skinny = M <= 16 && N * K * dtype_bytes(wt) >= kSklSplitMinWBytes;
+    const int64_t wbytes = N * K * dtype_bytes(wt);
+    const bool big_skinny =
+        (M <= 16 && wbytes >= kSklSplitMinWBytes) ||
+        (wt == MTP_FP8E4M3 && ((M <= 32 && wbytes >= kSklSplitMinWBytes) ||
+                               wbytes >= 2 * kSklSplitMinWBytes));
     if (pl.ok && (sklm == 1 || wide || big_skinny) && aligned && (!gamma || gt == MTP_F32)) {
       if (!ws || ws_bytes < pl.total) return MTP_ERR_WORKSPACE;
       SklArgs la{};
