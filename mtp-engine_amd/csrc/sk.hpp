@@ -100,6 +100,8 @@ __device__ __forceinline__ void sk_lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
                                            voff, soff, 0, AUX);
+#else
+  (void)r; (void)lds; (void)voff; (void)soff;
 #endif
 }
 
