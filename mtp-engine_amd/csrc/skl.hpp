@@ -353,21 +353,24 @@ skl_kernel(const SklArgs a) {
   __syncthreads();
   if (!s_flag) return;
   // last to arrive: sums in split order (its own terms from registers); the
-  // loads of QB splits at a time go out together
+  // loads of up to QB other splits go out together (one round trip for up
+  // to QB + 1 splits)
+  constexpr int QB = 4;
   f32x16 tot[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) tot[t][e] = 0.f;
   float sst = 0.f;
-  constexpr int QB = 2;  // splits per batch of loads
-  for (int q0 = 0; q0 < a.S; q0 += QB) {
+  bool own_in = false;
+  for (int r0 = 0; r0 < a.S - 1; r0 += QB) {
     f32x4 pv[QB][MT][4];
     float ps[QB];
 #pragma unroll
     for (int qq = 0; qq < QB; ++qq) {
-      const int q = q0 + qq;
-      const bool ld = q < a.S && q != sp;
+      const int r = r0 + qq;  // r-th other split
+      const int q = r + (r >= sp ? 1 : 0);
+      const bool ld = r < a.S - 1;
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -379,13 +382,14 @@ skl_kernel(const SklArgs a) {
     }
 #pragma unroll
     for (int qq = 0; qq < QB; ++qq) {
-      const int q = q0 + qq;
-      if (q >= a.S) break;
-      if (q == sp) {
+      const int r = r0 + qq;
+      if (r >= a.S - 1) break;
+      const int q = r + (r >= sp ? 1 : 0);
+      if (!own_in && sp < q) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) tot[t] += acc[t];
         sst += ssr;
-        continue;
+        own_in = true;
       }
 #pragma unroll
       for (int t = 0; t < MT; ++t)
@@ -395,6 +399,11 @@ skl_kernel(const SklArgs a) {
           for (int e = 0; e < 4; ++e) tot[t][4 * g4 + e] += pv[qq][t][g4][e];
       sst += ps[qq];
     }
+  }
+  if (!own_in) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tot[t] += acc[t];
+    sst += ssr;
   }
   set_rs(sst);
   finish(tot);
