@@ -275,7 +275,24 @@ __device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned ch
 #endif
 }
 
-template <int MT, int NA, int NWV>
+// Chunk swizzle of the weight rows in LDS (16-byte chunks of a 64-byte row).
+__device__ __forceinline__ int i4_swz(int r) { return (r >> 2) & 3; }
+
+// (a & m) | c in one v_and_or_b32 (m, c in registers).
+__device__ __forceinline__ uint32_t and_or_u32(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(m), "v"(c));
+  return d;
+}
+// A constant the compiler keeps in a VGPR (it cannot fold it back into a
+// literal operand).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  uint32_t d;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(d) : "s"(v));
+  return d;
+}
+
+template <int MT, int NA, int NWV, bool TWOS>
 __global__ void __launch_bounds__(64 * NWV, 1)
 int4_gemm_kernel(const I4Args a) {
   // NWV = 8: waves split each unit's k-steps in halves (wave = row quarter
@@ -332,11 +349,14 @@ int4_gemm_kernel(const I4Args a) {
   }
   const int nunits = a.K / UK;
 
-  // Weights: per unit the workgroup's BN rows x 64 bytes are copied to LDS
-  // row-major, 16 rows x 64 bytes per copy (copy c = wave + NWV i; lane L
-  // takes bytes 16 (L % 4) .. + 15 of row 16 c + L / 4). The MFMA A operand
-  // of subtile t is read back per lane: row wcol[t], bytes 32 h .. + 31 (16
-  // of them per k-half).
+  // Weights: per unit the workgroup's BN rows x 64 bytes are copied to LDS,
+  // 64 bytes per row, 16 rows x 64 bytes per copy (copy c = wave + NWV i);
+  // the 16-byte chunk j of row r sits at chunk j ^ i4_swz(r) of the row's
+  // 64 bytes, so lane L (LDS chunk L % 4 of row 16 c + L / 4) loads that
+  // row's chunk (L % 4) ^ i4_swz(row). The MFMA A operand of subtile t is
+  // read back per lane: row wcol[t], chunks 2 h, 2 h + 1 (one per k-half):
+  // the 16 lanes of a read take 16 consecutive rows at one chunk, which the
+  // swizzle spreads over all 64 banks (row-major they would hit 16 banks).
   const uint32_t ldw = (uint32_t)a.K / 2;
   const int nrows = min(BN, a.N - n0);
   const __amdgpu_buffer_rsrc_t wrs =
@@ -344,7 +364,8 @@ int4_gemm_kernel(const I4Args a) {
   uint32_t wvo[NWL];
 #pragma unroll
   for (int i = 0; i < NWL; ++i)
-    wvo[i] = (uint32_t)(16 * (wave + NWV * i) + (lane >> 2)) * ldw + 16u * (lane & 3);
+    wvo[i] = (uint32_t)(16 * (wave + NWV * i) + (lane >> 2)) * ldw +
+             16u * (uint32_t)((lane & 3) ^ i4_swz(16 * (wave + NWV * i) + (lane >> 2)));
   int wcol[NA];  // row of the lane inside the workgroup's BN
 #pragma unroll
   for (int t = 0; t < NA; ++t) wcol[t] = 32 * (NA * rq + t) + l32;
@@ -377,29 +398,30 @@ int4_gemm_kernel(const I4Args a) {
 
   // Vector-memory instruction v (0 <= v < NV) of unit `unit` into LDS
   // stage `slot`: weight copies first, then the scale copy, then x copies.
-  // Units past the last one copy with an out-of-range vector offset: zeros,
-  // no memory access (the scalar offset is not part of the descriptor's
-  // range check).
+  // Units past the last one copy through a descriptor of zero bytes: every
+  // offset is out of range, so zeros and no memory access (chosen with
+  // scalar selects, not per-lane offsets).
+  const __amdgpu_buffer_rsrc_t nrs = make_rsrc(a.packed, 0u);
   auto issue = [&](auto vc, int unit, int slot) __attribute__((always_inline)) {
     constexpr int v = decltype(vc)::value;
     const bool live = unit < nunits;
     const int su = live ? unit : 0;
     if constexpr (v < NWL) {
-      lds_copy16(wrs, xs + slot * STAGE + XST + (wave + NWV * v) * 1024, live ? wvo[v] : kOOB,
+      lds_copy16(live ? wrs : nrs, xs + slot * STAGE + XST + (wave + NWV * v) * 1024, wvo[v],
                  su * 64);
     } else if constexpr (v == NWL) {
       const int k = su * UK + 32 * srun;
       const int g = a.glog >= 0 ? k >> a.glog : k / a.group;
       unsigned char *dst = xs + slot * STAGE + XST + WST + srun * 1024 + shalf;
       if constexpr (KH) {
-        if (lane < BN / 16) lds_copy16(srs, dst, live ? svo : kOOB, (int)((uint32_t)g * ldst2));
+        if (lane < BN / 16) lds_copy16(live ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
       } else {
-        lds_copy16(srs, dst, live ? svo : kOOB, (int)((uint32_t)g * ldst2));
+        lds_copy16(live ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
       }
     } else {
       const int i = v - NWL - 1;
       const int c = wave + NWV * i;
-      lds_copy16(xrs, xs + slot * STAGE + (c >> 3) * TILE + (c & 7) * 1024, live ? xvo[i] : kOOB,
+      lds_copy16(live ? xrs : nrs, xs + slot * STAGE + (c >> 3) * TILE + (c & 7) * 1024, xvo[i],
                  su * TILE);
     }
   };
@@ -412,7 +434,10 @@ int4_gemm_kernel(const I4Args a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[t][j][e] = 0.f;
 
-  const uint32_t flip = a.nibble == MTP_NIBBLE_TWOS ? 0x88888888u : 0u;
+  // decode constants in registers: v_and_or_b32 takes no literal operand
+  // (VOP3), and with them it masks and ORs in one instruction
+  const uint32_t klo = opaque_u32(0x000F000Fu), khi = opaque_u32(0x00F000F0u),
+                 kmag = opaque_u32(0x64006400u);
   const h2 m1032 = h2{(_Float16)(-1032.0f), (_Float16)(-1032.0f)};
   const h2 m1152 = h2{(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
   // One unit: 8 k-steps, software-pipelined one step deep (the LDS reads
@@ -432,7 +457,8 @@ int4_gemm_kernel(const I4Args a) {
     for (int t = 0; t < NA; ++t)
 #pragma unroll
       for (int e = 0; e < NE; ++e)
-        wr[t][e] = *(const u32x4 *)(sw + wcol[t] * 64 + 32 * h + 16 * (KH ? kh : e));
+        wr[t][e] = *(const u32x4 *)(sw + wcol[t] * 64 +
+                                    16 * ((2 * h + (KH ? kh : e)) ^ i4_swz(wcol[t])));
     h2 s2[NA][NE];
 #pragma unroll
     for (int t = 0; t < NA; ++t)
@@ -445,13 +471,14 @@ int4_gemm_kernel(const I4Args a) {
     auto decode = [&](h8 (&af)[NA], int s) __attribute__((always_inline)) {
 #pragma unroll
       for (int t = 0; t < NA; ++t) {
-        const uint32_t w = wr[t][KH ? 0 : s >> 2][s & 3] ^ flip;
+        uint32_t w = wr[t][KH ? 0 : s >> 2][s & 3];
+        if constexpr (TWOS) w ^= 0x88888888u;  // two's complement -> offset-8
         const uint32_t w8 = w >> 8;
         const h2 sv = s2[t][KH ? 0 : s >> 2];
-        const uint32_t q0 = (w & 0x000F000Fu) | 0x64006400u;
-        const uint32_t q1 = (w & 0x00F000F0u) | 0x64006400u;
-        const uint32_t q2 = (w8 & 0x000F000Fu) | 0x64006400u;
-        const uint32_t q3 = (w8 & 0x00F000F0u) | 0x64006400u;
+        const uint32_t q0 = and_or_u32(w, klo, kmag);
+        const uint32_t q1 = and_or_u32(w, khi, kmag);
+        const uint32_t q2 = and_or_u32(w8, klo, kmag);
+        const uint32_t q3 = and_or_u32(w8, khi, kmag);
         u32x4 o;
         o[0] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, q0) + m1032) * sv);
         o[1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, q1) + m1152) * sv);

@@ -26,8 +26,9 @@ typedef void (*I4PrepKernel)(const void *, int64_t, int64_t, const void *, float
                              float *, int64_t, const void *, int, int64_t, int64_t, int64_t,
                              uint16_t *);
 // GEMM kernel for MT 32-row x tiles and 128 NA weight rows per workgroup
-// ((1, 1), (2, 1) or (4, 2)) with nw waves (4, or 8: k-halves), or null.
-I4Kernel int4_gemm_pick(int mt, int na, int nw);
+// ((1, 1), (2, 1) or (4, 2)) with nw waves (4, or 8: k-halves) for offset-8
+// or (twos) two's-complement nibbles, or null.
+I4Kernel int4_gemm_pick(int mt, int na, int nw, bool twos);
 // Prep kernel for x dtype xdt and gamma dtype gdt (-1: no gamma), or null.
 I4PrepKernel int4_prep(int xdt, int gdt);
 

@@ -733,7 +733,7 @@ int launch_int4(const void *x, int xdt, int64_t M, int64_t K, const uint8_t *pac
   // overrides (tuning)
   int nw = tl.mt == 4 ? 8 : 4;
   if (const char *e = std::getenv("MTP_INT4_WAVES")) nw = std::atoi(e) == 8 ? 8 : 4;
-  I4Kernel gemm = int4_gemm_pick(tl.mt, tl.na, nw);
+  I4Kernel gemm = int4_gemm_pick(tl.mt, tl.na, nw, nibble == MTP_NIBBLE_TWOS);
   if (!gemm) return MTP_ERR_DTYPE;
   const int64_t gn = (N + 128 * tl.na - 1) / (128 * tl.na);
   const int64_t blocks = (gn + 7) / 8 * 8 * tl.gm;
