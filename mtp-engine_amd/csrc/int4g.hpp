@@ -543,15 +543,21 @@ int4_gemm_kernel(const I4Args a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // k-halves: the waves of half 1 hand their sums to those of half 0
-  // through LDS (the stages are free now), [rq][t][j][lane]
-  f32x16 *red = (f32x16 *)xs;
+  // through LDS (the stages are free now)
+  // ([rq][t][j][quad][lane] of f32x4: 16 lanes touch 256 contiguous bytes)
+  f32x4 *red = (f32x4 *)xs;
   if constexpr (KH) {
     __syncthreads();
     if (kh == 1) {
 #pragma unroll
       for (int t = 0; t < NA; ++t)
 #pragma unroll
-        for (int j = 0; j < MT; ++j) red[((rq * NA + t) * MT + j) * 64 + lane] = acc[t][j];
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            red[(((rq * NA + t) * MT + j) * 4 + g) * 64 + lane] =
+                f32x4{acc[t][j][4 * g], acc[t][j][4 * g + 1], acc[t][j][4 * g + 2],
+                      acc[t][j][4 * g + 3]};
     }
     __syncthreads();
     if (kh == 1) return;
@@ -574,7 +580,7 @@ int4_gemm_kernel(const I4Args a) {
         float r4[4] = {acc[t][j][4 * g], acc[t][j][4 * g + 1], acc[t][j][4 * g + 2],
                        acc[t][j][4 * g + 3]};
         if constexpr (KH) {
-          const f32x4 o = ((const f32x4 *)&red[((rq * NA + t) * MT + j) * 64 + lane])[g];
+          const f32x4 o = red[(((rq * NA + t) * MT + j) * 4 + g) * 64 + lane];
 #pragma unroll
           for (int e = 0; e < 4; ++e) r4[e] += o[e];
         }

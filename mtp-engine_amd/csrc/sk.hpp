@@ -344,18 +344,31 @@ sk_kernel(const SkArgs a) {
 
   // ---- the four waves' partial tiles meet in LDS: wave w sums output tile
   // (u, t) = (w % 2, w / 2) (waves past the MT tiles only contribute)
-  f32x16 *red = (f32x16 *)lds;  // [wave][u][t][lane]
+  // [wave][u][t][quad][lane] of f32x4: a 16-lane group touches 256
+  // contiguous bytes (64 bytes per lane would put 4 lanes on each bank)
+  f32x4 *red = (f32x4 *)lds;
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) red[((wave * 2 + u) * MT + t) * 64 + lane] = acc[u][t];
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        red[(((wave * 2 + u) * MT + t) * 4 + g4) * 64 + lane] =
+            f32x4{acc[u][t][4 * g4], acc[u][t][4 * g4 + 1], acc[u][t][4 * g4 + 2],
+                  acc[u][t][4 * g4 + 3]};
   __syncthreads();
   f32x16 v;
 #pragma unroll
   for (int e = 0; e < 16; ++e) v[e] = 0.f;
   if (owner) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v += red[((q * 2 + ou) * MT + ot) * 64 + lane];
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4 p = red[(((q * 2 + ou) * MT + ot) * 4 + g4) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * g4 + e] += p[e];
+      }
   }
 
   // lane's outputs: v[e] = D[n][m], m = 32 ot + lane % 32,
