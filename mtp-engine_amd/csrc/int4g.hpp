@@ -380,6 +380,12 @@ int4_gemm_kernel(const I4Args a) {
   const __amdgpu_buffer_rsrc_t srs =
       make_rsrc((const uint16_t *)a.scales + n0, (uint32_t)(a.ng * a.ldst - n0) * 2u);
   const int srun = KH ? wave & 3 : wave;
+  // a group of a multiple of 128 k covers the whole unit: its four runs
+  // share one scale per row, so only run 0 is copied and read (the other
+  // copies go to the zero-byte descriptor, keeping the per-unit count of
+  // vector-memory instructions of every wave)
+  const bool one_run = a.group % 128 == 0;
+  const bool scopy = !one_run || srun == 0;
   const uint32_t shalf = KH ? (uint32_t)(wave >> 2) * BN : 0u;  // bytes
   const uint32_t svo = lane < BN / 8 ? (uint32_t)lane * 16u + shalf : kOOB;
   const uint32_t ldst2 = (uint32_t)a.ldst * 2u;
@@ -414,9 +420,10 @@ int4_gemm_kernel(const I4Args a) {
       const int g = a.glog >= 0 ? k >> a.glog : k / a.group;
       unsigned char *dst = xs + slot * STAGE + XST + WST + srun * 1024 + shalf;
       if constexpr (KH) {
-        if (lane < BN / 16) lds_copy16(live ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
+        if (lane < BN / 16)
+          lds_copy16(live && scopy ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
       } else {
-        lds_copy16(live ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
+        lds_copy16(live && scopy ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
       }
     } else {
       const int i = v - NWL - 1;
@@ -464,7 +471,8 @@ int4_gemm_kernel(const I4Args a) {
     for (int t = 0; t < NA; ++t)
 #pragma unroll
       for (int g = 0; g < NE; ++g) {
-        const _Float16 f = *(const _Float16 *)(ss + (2 * h + (KH ? kh : g)) * 1024 + wcol[t] * 2);
+        const int run = one_run ? 0 : 2 * h + (KH ? kh : g);
+        const _Float16 f = *(const _Float16 *)(ss + run * 1024 + wcol[t] * 2);
         s2[t][g] = h2{f, f};
       }
     // wave k-step s (0 .. KSW - 1) is k-step 4 kh + s of the unit
