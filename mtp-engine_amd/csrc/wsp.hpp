@@ -474,29 +474,10 @@ wsp_kernel(const WsArgs a) {
   __syncthreads();
   if (!s_flag) return;
   // The last workgroup sums the splits in split order; loads go out four
-  // splits at a time (past the last split: zeros) so their latencies overlap.
-  if (th < MPAD) {
-    float ss = 0.f;
-    for (int q0 = 0; q0 < a.S; q0 += 4) {
-      float t4[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int q = q0 + j < a.S ? q0 + j : q0;
-        t4[j] = get_f32(sqp + ((int64_t)grp * a.S + q) * MPAD + th);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (q0 + j < a.S) ss += t4[j];
-    }
-    sq_row[th] = ss;
-  }
-  __syncthreads();
-  load_factors();
-  f32x4 v[IPT];
-#pragma unroll
-  for (int it = 0; it < IPT; ++it) v[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int q0 = 0; q0 < a.S; q0 += 4) {
-    f32x4 t4[IPT][4];
+  // splits at a time (past the last split: zeros) so their latencies
+  // overlap, the first four before the row statistics are read.
+  f32x4 t4[IPT][4];
+  auto load_batch = [&](int q0) __attribute__((always_inline)) {
 #pragma unroll
     for (int it = 0; it < IPT; ++it)
 #pragma unroll
@@ -508,10 +489,36 @@ wsp_kernel(const WsArgs a) {
         t4[it][j] =
             __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kSc1));
       }
+  };
+  load_batch(0);
+  if (th < MPAD) {
+    float ss = 0.f;
+    for (int q0 = 0; q0 < a.S; q0 += 4) {
+      float s4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int q = q0 + j < a.S ? q0 + j : q0;
+        s4[j] = get_f32(sqp + ((int64_t)grp * a.S + q) * MPAD + th);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (q0 + j < a.S) ss += s4[j];
+    }
+    sq_row[th] = ss;
+  }
+  __syncthreads();
+  load_factors();
+  f32x4 v[IPT];
+#pragma unroll
+  for (int it = 0; it < IPT; ++it) v[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q0 = 0;;) {
 #pragma unroll
     for (int it = 0; it < IPT; ++it)
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[it] += t4[it][j];
+    q0 += 4;
+    if (q0 >= a.S) break;
+    load_batch(q0);
   }
 #pragma unroll
   for (int it = 0; it < IPT; ++it) {
