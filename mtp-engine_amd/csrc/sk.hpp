@@ -425,19 +425,37 @@ sk_kernel(const SkArgs a) {
   __syncthreads();
   if (!s_flag) return;
   if (owner) {
+    // sums in split order (its own term from registers); the loads of QB
+    // splits go out together, one round trip for up to QB splits
+    constexpr int QB = 4;
     f32x16 tot;
 #pragma unroll
     for (int e = 0; e < 16; ++e) tot[e] = 0.f;
-    for (int q = 0; q < a.S; ++q) {
-      f32x4 pv[4];
+    for (int q0 = 0; q0 < a.S; q0 += QB) {
+      f32x4 pv[QB][4];
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
-        pv[g4] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, part_off(q, g4), 0, kSc1));
+      for (int qq = 0; qq < QB; ++qq) {
+        const int q = q0 + qq;
+        const bool ld = q < a.S && q != sp;
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
+        for (int g4 = 0; g4 < 4; ++g4)
+          pv[qq][g4] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, ld ? part_off(q, g4) : kOOB, 0,
+                                                           kSc1));
+      }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tot[4 * g4 + e] += pv[g4][e];
+      for (int qq = 0; qq < QB; ++qq) {
+        const int q = q0 + qq;
+        if (q >= a.S) break;
+        if (q == sp) {
+          tot += v;
+          continue;
+        }
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tot[4 * g4 + e] += pv[qq][g4][e];
+      }
     }
     finish(tot);
   }
