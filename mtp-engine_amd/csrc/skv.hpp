@@ -65,6 +65,7 @@ skv_kernel(const SkvArgs a) {
   __shared__ unsigned long long s_key[8][64];
   __shared__ int s_flag;
   __shared__ int s_top[64];
+  __shared__ int s_draft[64];
 
   const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
   const int N = a.N, K = a.K, nst = a.nst;
@@ -243,6 +244,13 @@ skv_kernel(const SkvArgs a) {
   if (th == 0) s_flag = ticket_add(a.ticket) == (unsigned)(grid - 1);
   __syncthreads();
   if (!s_flag) return;
+  // the drafts (fewer than the rows) go to LDS with the same round trip as
+  // the row keys; read in the acceptance chain, they would be re-read from
+  // memory after every accept store (byte stores may alias them)
+  {
+    const int nd = a.multi ? a.M / a.S_seq * a.D : a.M;
+    if (th < nd && a.draft) s_draft[th] = a.draft[th];
+  }
   for (int m = th; m < a.M; m += 512) {
     const unsigned long long k =
         __hip_atomic_load(a.keys + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -253,7 +261,7 @@ skv_kernel(const SkvArgs a) {
   if (a.top)
     for (int m = th; m < a.M; m += 512) a.top[m] = s_top[m];
   if (!a.multi) {
-    for (int m = th; m < a.M; m += 512) a.accept[m] = (int8_t)(s_top[m] == a.draft[m]);
+    for (int m = th; m < a.M; m += 512) a.accept[m] = (int8_t)(s_top[m] == s_draft[m]);
   } else {
     const int Sq = a.S_seq, Dd = a.D;
     for (int bl = th; bl < a.M / Sq; bl += 512) {
@@ -261,7 +269,7 @@ skv_kernel(const SkvArgs a) {
       a.corrected[bl] = tp[0];
       int n = 0;
       for (int d = 0; d < Dd; ++d) {
-        const bool ok = (tp[d + 1] == a.draft[(int64_t)bl * Dd + d]) && (n == d);
+        const bool ok = (tp[d + 1] == s_draft[bl * Dd + d]) && (n == d);
         a.accept[(int64_t)bl * Dd + d] = (int8_t)ok;
         if (ok) n = d + 1;
       }
