@@ -74,6 +74,21 @@ const char *mtp_status_string(int status);
 /* Name of the last HIP error seen by a failed launch on this thread. */
 const char *mtp_last_hip_error(void);
 
+/*
+ * Launch-planning overrides, process-wide (no counterpart in the reference,
+ * whose Triton launches take tile sizes from KernelTuningConfig,
+ * mtp_kernels.py:54-103). Keys: "skl" (1 force / 0 disable the single-launch
+ * skinny kernel), "sk_splits", "ws_variant", "ws_splits", "skl_waves" (4 or
+ * 8), "skl_splits", "attn_chunk_blocks", "int4_waves" (4 or 8),
+ * "verify_wstream" (1 = column-group verify kernel). value -1 restores the
+ * planner's choice. The MTP_SKL, MTP_SK_SPLITS, MTP_WS_TUNE ("variant,splits"),
+ * MTP_SKL_WAVES, MTP_SKL_SPLITS, MTP_ATTN_CHUNK_BLOCKS, MTP_INT4_WAVES and
+ * MTP_VERIFY_WSTREAM environment variables seed the keys once, at the
+ * first launch plan. MTP_ERR_ARG for an unknown key.
+ */
+int mtp_set_tuning(const char *name, int64_t value);
+int mtp_get_tuning(const char *name, int64_t *value);
+
 /* ------------------------------------------------------------------------- */
 /* RMSNorm -> linear family                                                  */
 /* ------------------------------------------------------------------------- */
@@ -82,8 +97,9 @@ const char *mtp_last_hip_error(void);
  * Replaces fused_rmsnorm_linear(x, weight, bias=None, eps=1e-6, scale=None)
  * (mtp_kernels.py:936-977; eager twin _eager_rmsnorm_linear 778-787):
  *   y = cast_xdtype(((x * rsqrt(mean(x^2) + eps) * gamma) @ W^T + bias) * scale)
- * x [M, K] in x_dtype (F32, BF16, F16); weight [N, K] in w_dtype (must equal
- * x_dtype); bias [N] in bias_dtype or NULL (the reference casts bias to
+ * x [M, K] in x_dtype (F32, BF16, F16); weight [N, K] in w_dtype (any float
+ * dtype; the tiled kernels take w_dtype == x_dtype with 16-byte aligned
+ * rows, everything else runs an exact fp32 fallback); bias [N] in bias_dtype or NULL (the reference casts bias to
  * x.dtype first, mtp_kernels.py:952: the caller passes it already cast);
  * gamma [K] in gamma_dtype or NULL (keyword extension; NULL = the reference);
  * norm = 0 skips the RMSNorm (the no-norm mode CachedLinear needs,
@@ -155,8 +171,11 @@ size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M,
  *   top[m] = argmax_v(hidden[m] . W[v] + bias[v])  (lowest index on ties,
  *            NaN counts as the maximum, as torch.argmax)
  *   accept[m] = (top[m] == draft[m])
- * hidden [M, K] (F32/BF16/F16), weight [V, K] same dtype, bias [V] or NULL,
- * draft [M] int32 -> accept [M] int8, top [M] int32. Logits never reach HBM.
+ * hidden [M, K] and weight [V, K] in any float dtypes (F32/BF16/F16; both
+ * upcast to fp32 as the reference does), bias [V] or NULL, draft [M] int32
+ * -> accept [M] int8, top [M] int32. Any K and element alignment (16-bit
+ * same-dtype operands with 16-byte rows take the streaming kernels, the
+ * rest a generic kernel). Logits never reach HBM.
  */
 int mtp_fused_verify(const void *hidden, int h_dtype, int64_t M, int64_t K,
                      const void *weight, int w_dtype, int64_t V,
@@ -300,6 +319,57 @@ int mtp_dequantize_int4(const uint8_t *packed, const void *scales,
                         int scale_dtype, int64_t N, int64_t K, int64_t group,
                         float *out, void *stream);
 
+/*
+ * Replaces fused_causal_attention(q, k, v, scale=None)
+ * (mtp_kernels.py:980-1011; kernel 235-298; eager 790-801):
+ *   out[b, h] = softmax_l(q[b, h] . k[b, h, l] * scale) @ v[b, h, l]
+ * (a single query at the last position: every key is attended).
+ * q / out [B, H, D], k / v [B, H, L, D], one float dtype. Workspace as
+ * mtp_attention_workspace_bytes(dtype, B, 1, H, D, 0, L).
+ */
+int mtp_fused_causal_attention(const void *q, int dtype, int64_t B, int64_t H,
+                               int64_t D, const void *k, const void *v,
+                               int64_t L, float scale, void *out,
+                               void *workspace, size_t workspace_bytes,
+                               void *stream);
+
+/*
+ * Replaces fused_causal_attention_fp8(q, k_fp8, v_fp8, kscale, vscale,
+ * scale=None) (mtp_kernels.py:1105-1133; kernel 373-427; eager 817-829):
+ * k / v fp8 e4m3fn [B, H, L, D] dequantised per head by kscale[H] /
+ * vscale[H] (fp32); q / out [B, H, D] in dtype. No workspace.
+ */
+int mtp_fused_causal_attention_fp8(const void *q, int dtype, int64_t B,
+                                   int64_t H, int64_t D, const void *k_fp8,
+                                   const void *v_fp8, int64_t L,
+                                   const float *kscale, const float *vscale,
+                                   float scale, void *out, void *stream);
+
+/*
+ * Replaces fused_tree_attn_rmsnorm_linear(q, k, v, mask, proj_w, rms_w=None,
+ * proj_bias=None, wscale=None, scale=None, eps=1e-6)
+ * (mtp_kernels.py:1222-1250; eager _eager_tree_attn_rmsnorm_linear 881-907):
+ *   a[b, h] = masked single-query attention (as mtp_fused_tree_attention)
+ *   out[b, h] = (a * rsqrt(mean_d(a^2) + eps) * rms_w) @ (proj_w * wscale)^T + proj_bias
+ * q [B, H, D], k / v [B, H, L, D], mask [L]; proj_w [N, D] (float, or fp8
+ * with wscale [N]); rms_w [D] or NULL (ones); proj_bias [N] or NULL;
+ * out [B, H, N] in q's dtype. A mask that admits no key gives NaN rows,
+ * like the eager twin, deterministically. Two launches (attention into the
+ * workspace, then the RMSNorm -> linear kernel over the B * H rows).
+ */
+int mtp_fused_tree_attn_rmsnorm_linear(
+    const void *q, int dtype, int64_t B, int64_t H, int64_t D, const void *k,
+    const void *v, int64_t L, const void *mask, int mask_dtype,
+    const void *proj_w, int w_dtype, int64_t N, const void *rms_w,
+    int rms_dtype, const void *proj_bias, int bias_dtype, const float *wscale,
+    float scale, float eps, void *out, void *workspace, size_t workspace_bytes,
+    void *stream);
+/* w_kind: proj_w's dtype, or MTP_FP8E4M3 whenever wscale is passed. */
+size_t mtp_tree_attn_rmsnorm_linear_workspace_bytes(int dtype, int64_t B,
+                                                    int64_t H, int64_t D,
+                                                    int64_t L, int w_kind,
+                                                    int64_t N);
+
 /* Workspace bytes for the attention entry points: B batch rows, NQ queries
  * per (batch, head) (1 for the two reference functions, N for tree verify),
  * Lc context keys, Lt dense keys (L of fused_tree_attention, N of tree
@@ -307,6 +377,110 @@ int mtp_dequantize_int4(const uint8_t *packed, const void *scales,
 size_t mtp_attention_workspace_bytes(int dtype, int64_t B, int64_t NQ,
                                      int64_t H, int64_t D, int64_t Lc,
                                      int64_t Lt);
+
+/* ------------------------------------------------------------------------- */
+/* Draft chain                                                               */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Replaces fused_rmsnorm(x, weight=None, eps=1e-6)
+ * (mtp_kernels.py:910-933; kernel 120-146; eager _eager_rmsnorm 771-775):
+ *   y = x * rsqrt(mean(x^2) + eps) * weight   (fp32, rounded to dtype)
+ * x / y [M, N] contiguous in dtype; weight [N] in w_dtype or NULL (ones).
+ * The reference casts weight to x's dtype first: the caller passes it cast.
+ */
+int mtp_fused_rmsnorm(const void *x, int dtype, int64_t M, int64_t N,
+                      const void *weight, int w_dtype, float eps, void *y,
+                      void *stream);
+
+/*
+ * Replaces fused_add_rmsnorm(x, residual, weight=None, eps=1e-6)
+ * (mtp_kernels.py:1082-1102; kernel 1050-1070; eager 1073-1079):
+ *   s = x + residual (fp32);  y = s * rsqrt(mean(s^2) + eps) * weight
+ * (the draft chain's combine-norm, combine_norm(hidden + emb) at
+ * mtp_engine.py:241, 757, in one pass; fp32 addition, where the module
+ * rounds the sum to the hidden dtype first).
+ */
+int mtp_fused_add_rmsnorm(const void *x, const void *residual, int dtype,
+                          int64_t M, int64_t N, const void *weight,
+                          int w_dtype, float eps, void *y, void *stream);
+
+/*
+ * Replaces argmax_greedy(logits) / sample_token(logits, temperature <= 0)
+ * (mtp_perf_hardening.py:170-186; the engine's _sample_tokens,
+ * mtp_engine.py:722-726) and the embedding lookup of the next draft step
+ * (mtp_engine.py:750, 773):
+ *   tokens[m] = argmax_v logits[m, v]   (torch.argmax order, int64)
+ *   emb_out[m, :] = emb_table[tokens[m], :]   (when emb_table is not NULL)
+ * logits [M, V] with row stride ld elements; emb_table [table_rows, H].
+ * Needs mtp_argmax_workspace_bytes(M, V) of workspace.
+ */
+int mtp_argmax(const void *logits, int dtype, int64_t M, int64_t V,
+               int64_t ld, int64_t *tokens, const void *emb_table,
+               int table_dtype, int64_t table_rows, int64_t H, void *emb_out,
+               void *workspace, size_t workspace_bytes, void *stream);
+size_t mtp_argmax_workspace_bytes(int64_t M, int64_t V);
+
+/* ------------------------------------------------------------------------- */
+/* KV step after verify                                                      */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Batched form of PagedKVCache.write_inplace (mtp_engine.py:581-585):
+ *   pages[table[b, p], b, h, p % page_size, :] = new[b, t, h, :],  p = start + t
+ * for k and v. new: [B, T, H, D] by element strides (s_sb, s_st, s_sh), d
+ * contiguous, in src_dtype; pages [num_pages, B, H, page_size, D] in
+ * dst_dtype (converted as .to(dtype)); page_table [B, ld_tab] int32. start
+ * is start_dev[b] (start_per_row = 1) or start_dev[0] (a device scalar,
+ * e.g. the KV length mtp_verify_commit maintains), or start_host when
+ * start_dev is NULL. Positions outside the table and pages outside
+ * [0, num_pages) are skipped.
+ */
+int mtp_paged_kv_write(const void *k_new, const void *v_new, int src_dtype,
+                       int64_t B, int64_t T, int64_t H, int64_t D,
+                       int64_t s_sb, int64_t s_st, int64_t s_sh, void *k_pages,
+                       void *v_pages, int dst_dtype, int64_t num_pages,
+                       int64_t page_size, const int32_t *page_table,
+                       int64_t ld_tab, const int64_t *start_dev,
+                       int start_per_row, int64_t start_host, void *stream);
+
+/*
+ * The verify consumer of generate_fused / generate_optimized
+ * (mtp_engine.py:1244-1258, 1328-1344) with its KVManager rollback / commit
+ * (275-331) on the device, without the host reads of accepted_n and accept:
+ *   a_n = min_b accepted_n[b];  reject = any accept[b, d] == 0
+ *   width = reject ? a_n + 1 : D
+ *   tokens[b, :width] = reject ? draft[b, :a_n] ++ corrected[b] : draft[b]
+ *   tokens[b, width:] = -1;  *kv_len = *checkpoint + width;  *width_out = width
+ * and, when ids is not NULL, ids[b, *ids_len + j] = tokens[b, j] (j < width,
+ * inside ld_ids) and *ids_len += width. tokens [B, D + 1] int64; draft
+ * [B, D] int32 or int64; checkpoint / kv_len / ids_len are int64 device
+ * scalars (kv_len may alias checkpoint). One workgroup.
+ */
+int mtp_verify_commit(const int8_t *accept, const int32_t *accepted_n,
+                      const int32_t *corrected, const void *draft,
+                      int draft_dtype, int64_t B, int64_t D,
+                      const int64_t *checkpoint, int64_t *kv_len,
+                      int64_t *tokens, int32_t *width_out, int64_t *ids,
+                      int64_t ld_ids, int64_t *ids_len, void *stream);
+
+/*
+ * Replaces RadixKVCache.batch_prefix_match(ids) (mtp_radix.py:195-272,
+ * kernel 254-267): out[r] = first column c with ids[r, c] != ids[0, c], or
+ * L when the row equals row 0; all zeros when R <= 1. ids [R, L] int64,
+ * out [R] int32.
+ */
+int mtp_batch_prefix_match(const int64_t *ids, int64_t R, int64_t L,
+                           int32_t *out, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Workspace                                                                 */
+/* ------------------------------------------------------------------------- */
+
+/* Zero a workspace with a kernel launch on `stream` (no memset node when the
+ * stream is being captured). workspace 16-byte aligned, bytes % 4 == 0.
+ * No counterpart in the reference (whose wrappers allocate per call). */
+int mtp_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -416,6 +416,11 @@ attn_merge_kernel(const AttnArgs a) {
 // Fallback for shapes the MFMA kernel does not take (fp32 q / k / v, head
 // dims other than 64 / 128, more than 64 queries): one wave per (b, query,
 // h), keys in order, lanes split d. Same semantics and key sources.
+__device__ __forceinline__ float load_kv_f32(const void *p, int dt, int64_t i) {
+  if (dt == MTP_FP8E4M3) return __builtin_amdgcn_cvt_f32_fp8((uint32_t)((const uint8_t *)p)[i], 0);
+  return load_as_f32(p, dt, i);
+}
+
 __global__ void __launch_bounds__(64) attn_generic_kernel(const AttnArgs a, int D, int ct) {
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
@@ -431,6 +436,10 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(const AttnArgs a, int 
   }
   float m = -INFINITY, l = 0.f;
   const int total = a.Lc + a.Lt;
+  // K / V in q's dtype, or fp8 with per-head scales (scores and values are
+  // scaled in fp32 after the dot products)
+  const int kdt = a.kv_fp8 ? MTP_FP8E4M3 : ct;
+  const float ks = a.kscale ? a.kscale[h] : 1.f, vs = a.vscale ? a.vscale[h] : 1.f;
   for (int t = 0; t < total; ++t) {
     int64_t off;
     const void *kb, *vb;
@@ -453,11 +462,11 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(const AttnArgs a, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = lane + 64 * i;
-      if (d < D) sp += qv[i] * load_as_f32(kb, ct, off + d);
+      if (d < D) sp += qv[i] * load_kv_f32(kb, kdt, off + d);
     }
 #pragma unroll
     for (int w = 32; w > 0; w >>= 1) sp += __shfl_xor(sp, w, 64);
-    const float s = ok ? sp * a.scale : -INFINITY;
+    const float s = ok ? sp * ks * a.scale : -INFINITY;
     const float mn = fmaxf(m, s);
     const bool none = mn == -INFINITY;
     const float alpha = none ? 1.f : __expf(m - mn);
@@ -467,7 +476,7 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(const AttnArgs a, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = lane + 64 * i;
-      ov[i] = ov[i] * alpha + (d < D ? p * load_as_f32(vb, ct, off + d) : 0.f);
+      ov[i] = ov[i] * alpha + (d < D ? p * (load_kv_f32(vb, kdt, off + d) * vs) : 0.f);
     }
   }
   const int64_t ooff = (int64_t)b * a.o_sb + (int64_t)qi * a.o_sn + (int64_t)h * a.o_sh;

@@ -29,6 +29,8 @@ struct AttnArgs {
   int64_t o_sb, o_sn, o_sh;
   int B, NQ, H;
   float scale;
+  int kv_fp8;                  // 1: K / V are fp8 e4m3 (fallback kernel only), 0: q's dtype
+  const float *kscale, *vscale;  // per-head K / V scales [H] (fp8 KV) or null
   int nchunks, chunk_blocks;   // blocks of kAttnBlock keys (context, then dense) per chunk
   float *part;                 // [B*H][nchunks][16*ceil(NQ/16)][D]
   float *ml;                   // [B*H][nchunks][16*ceil(NQ/16)][2]

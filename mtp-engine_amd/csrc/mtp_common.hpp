@@ -198,15 +198,18 @@ __device__ __forceinline__ u32x4 ld_nt16(const void *p) {
 }
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
 
-// ---- cross-workgroup hand-off without an L2 write-back ---------------------
-// An agent-scope release fence writes back the whole L2 of the XCD
-// (buffer_wbl2), which serialises badly when every workgroup of a launch
-// does it. Data handed between workgroups is therefore only ever accessed
-// through agent-scope atomics (global_load/store ... sc1: coherent across
-// XCDs): the producer publishes with atomic stores, waits until they have
-// completed (s_waitcnt), then bumps the arrival ticket with a relaxed atomic
-// RMW (performed at the device coherence point); the consumer that sees the
-// final count reads the data back with agent-scope atomic loads.
+// ---- cross-workgroup hand-off ----------------------------------------------
+// Data handed between workgroups is only ever accessed through agent-scope
+// atomics or sc1 buffer accesses (coherent across XCDs at the device
+// coherence point): the producer publishes, waits until its stores have
+// completed (s_waitcnt), meets its workgroup at a barrier, then one thread
+// bumps the arrival ticket with a release RMW; the workgroup that sees the
+// final count runs an agent-scope acquire fence before it reads the data
+// back. The release / acquire pair is what orders the data under the HIP
+// memory model (the relaxed accesses alone are not ordered with the ticket);
+// on gfx950 it costs one L2 write-back (buffer_wbl2 sc1) per arriving
+// workgroup, of the few lines its own plain stores left dirty, and one L2
+// invalidate (buffer_inv sc1) in the last workgroup.
 __device__ __forceinline__ void pub_f32(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -221,9 +224,13 @@ __device__ __forceinline__ int get_i32(const int *p) {
 }
 // Every thread: wait for its own stores/atomics to complete.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
-// Relaxed arrival count (returns the previous value).
+// Arrival count with release semantics (returns the previous value).
 __device__ __forceinline__ unsigned ticket_add(unsigned *t) {
-  return __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The last workgroup to arrive: acquire what the others released.
+__device__ __forceinline__ void handoff_acquire() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 __device__ __forceinline__ void ticket_reset(unsigned *t) {
   __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

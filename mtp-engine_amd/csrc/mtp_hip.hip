@@ -7,7 +7,9 @@
 #include <algorithm>
 #include <atomic>
 #include <cstring>
+#include <mutex>
 
+#include "abi_util.hpp"
 #include "attn_args.hpp"
 #include "generic.hpp"
 #include "int4g_args.hpp"
@@ -15,33 +17,78 @@
 #include "sk_args.hpp"
 #include "skl_args.hpp"
 #include "skv_args.hpp"
+#include "vgen.hpp"
 #include "ws_dispatch.hpp"
+
+namespace mtp {
+thread_local char g_last_hip_error[256] = "";
+
+namespace {
+std::atomic<int> g_tune[kTuneCount];
+std::once_flag g_tune_once;
+const char *const kTuneNames[kTuneCount] = {
+    "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
+    "attn_chunk_blocks", "int4_waves", "verify_wstream"};
+
+int env_int(const char *name, int dflt) {
+  const char *e = std::getenv(name);
+  return (e && *e) ? std::atoi(e) : dflt;
+}
+
+void tune_init() {
+  for (auto &t : g_tune) t.store(-1, std::memory_order_relaxed);
+  if (const char *e = std::getenv("MTP_SKL")) {
+    if (*e) g_tune[kTuneSkl].store(*e == '0' ? 0 : 1, std::memory_order_relaxed);
+  }
+  g_tune[kTuneSkSplits].store(env_int("MTP_SK_SPLITS", -1), std::memory_order_relaxed);
+  if (const char *e = std::getenv("MTP_WS_TUNE")) {
+    int v = -1, sp = -1;
+    if (*e && std::sscanf(e, "%d,%d", &v, &sp) >= 1) {
+      g_tune[kTuneWsVariant].store(v, std::memory_order_relaxed);
+      g_tune[kTuneWsSplits].store(sp, std::memory_order_relaxed);
+    }
+  }
+  g_tune[kTuneSklWaves].store(env_int("MTP_SKL_WAVES", -1), std::memory_order_relaxed);
+  g_tune[kTuneSklSplits].store(env_int("MTP_SKL_SPLITS", -1), std::memory_order_relaxed);
+  g_tune[kTuneAttnChunkBlocks].store(env_int("MTP_ATTN_CHUNK_BLOCKS", -1),
+                                     std::memory_order_relaxed);
+  g_tune[kTuneInt4Waves].store(env_int("MTP_INT4_WAVES", -1), std::memory_order_relaxed);
+  if (const char *e = std::getenv("MTP_VERIFY_WSTREAM"))
+    if (*e) g_tune[kTuneVerifyWstream].store(1, std::memory_order_relaxed);
+}
+}  // namespace
+
+int tune(TuneKey k) {
+  std::call_once(g_tune_once, tune_init);
+  return g_tune[k].load(std::memory_order_relaxed);
+}
+
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        c <= 0)
+      c = 256;
+    cache[dev].store(c, std::memory_order_relaxed);
+    v = c;
+  }
+  return v;
+}
+}  // namespace mtp
 
 using namespace mtp;
 
 namespace {
 
-thread_local char g_last_hip_error[256] = "";
-
-int launch_status() {
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess) return MTP_OK;
-  std::strncpy(g_last_hip_error, hipGetErrorString(e), sizeof(g_last_hip_error) - 1);
-  return MTP_ERR_LAUNCH;
-}
-
-bool is_float_dt(int dt) { return dt == MTP_F32 || dt == MTP_BF16 || dt == MTP_F16; }
-bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
-
-// Tuning override for sweeps: MTP_WS_TUNE="variant,splits" (-1 = default).
+// Row-chunk kernel overrides for sweeps (variant, splits; -1 = the plan's).
 void tune_override(int &variant, int &splits) {
-  const char *s = std::getenv("MTP_WS_TUNE");
-  if (!s || !*s) return;
-  int v = -1, sp = -1;
-  if (std::sscanf(s, "%d,%d", &v, &sp) >= 1) {
-    if (v >= 0) variant = v;
-    if (sp > 0) splits = sp;
-  }
+  const int v = tune(kTuneWsVariant), sp = tune(kTuneWsSplits);
+  if (v >= 0) variant = v;
+  if (sp > 0) splits = sp;
 }
 
 typedef WsVariant Variant;
@@ -56,9 +103,8 @@ bool fast_pair(int ct, int wt) {
   return wt == ct || wt == MTP_FP8E4M3;
 }
 
-constexpr int kTargetBlocks = 512;  // 2 workgroups per CU on 256 CUs
-constexpr size_t kCounterBytes = MTP_WORKSPACE_COUNTER_BYTES;
-constexpr int64_t kCounterSlots = (int64_t)(kCounterBytes / 4);
+// 2 workgroups per CU
+int target_blocks() { return 2 * device_cus(); }
 
 struct Plan {
   bool generic = true;
@@ -69,7 +115,6 @@ struct Plan {
   size_t part_off = 0, sqp_off = 0, ticket_off = 0, aval_off = 0, aidx_off = 0, total = 0;
 };
 
-size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Launch plan for the weight-streaming kernel. `rows_per_chunk` rows of x go
 // to each blockIdx.y chunk. epi == EPI_ARGMAX forces S == 1.
@@ -103,7 +148,7 @@ Plan make_plan(int ct, int wt, int64_t M, int64_t N, int64_t K, int epi, int row
   int S = 1;
   if (epi == EPI_LINEAR) {
     const int rounds = (p.nkb + p.var.wk - 1) / p.var.wk;
-    S = splits > 0 ? splits : (kTargetBlocks + p.G * p.chunks / 2) / (p.G * p.chunks);
+    S = splits > 0 ? splits : (target_blocks() + p.G * p.chunks / 2) / (p.G * p.chunks);
     if (S < 1) S = 1;
     if (S > rounds) S = rounds;
     // split-K needs one counter per (chunk, group) in the counter prefix
@@ -174,7 +219,8 @@ int launch_ws(const Plan &p, WsArgs &a, int epi, void *ws, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // Pipelined linear kernel: plan and launch.
 constexpr size_t kLdsMax = 150 * 1024;  // dynamic LDS limit we allow
-constexpr int kWspMinBlocks = 200;      // aim for most of the 256 CUs busy
+// aim for most of the CUs busy (200 of 256)
+int wsp_min_blocks() { return device_cus() * 200 / 256; }
 
 struct PlanX {
   bool ok = false;
@@ -253,7 +299,7 @@ PlanX make_plan_x(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   } else {
     // more K-splits while the grid is short of CUs and every K-group keeps
     // >= 4 stages
-    while ((int64_t)p.G * S * p.chunks < kWspMinBlocks && p.nkb / (S + 1) >= 4 * p.var.wk) ++S;
+    while ((int64_t)p.G * S * p.chunks < wsp_min_blocks() && p.nkb / (S + 1) >= 4 * p.var.wk) ++S;
   }
   if (S > p.nkb) S = p.nkb;
   if (S > 1 && (int64_t)p.chunks * p.G > kCounterSlots) return p;
@@ -303,7 +349,7 @@ int launch_wsp(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
   const hipError_t e = hipFuncSetAttribute((const void *)k,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
   if (e != hipSuccess) {
-    std::strncpy(g_last_hip_error, hipGetErrorString(e), sizeof(g_last_hip_error) - 1);
+    note_hip_error(e);
     return MTP_ERR_LAUNCH;
   }
   const int threads = p.var.wn * p.var.wk * 64;
@@ -323,7 +369,8 @@ struct PlanSk {
   size_t xf_off = 0, part_off = 0, total = 0;
 };
 
-constexpr int kSkMinBlocks = 200;  // aim for most of the 256 CUs busy
+// aim for most of the CUs busy (200 of 256)
+int sk_min_blocks() { return device_cus() * 200 / 256; }
 constexpr int kSkMinStages = 4;    // stages per split at least
 
 // Tile: 64 columns x all rows of x (<= 64); K-splits only while the grid is
@@ -337,10 +384,10 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   if (wt != MTP_FP8E4M3 && wt != ct) return p;
   // 17 .. 64 rows: the row-chunk kernel (wsp) is faster below that
   // (fp8 K 4096 N 14336: 8 rows 19.3 us wsp / 20.8 sk, 32 rows 25.5 / 21.2)
-  const char *force = std::getenv("MTP_SK_SPLITS");
-  const bool forced = force && *force;
+  const int force = tune(kTuneSkSplits);
+  const bool forced = force > 0;
   if (M <= 0 || M > 64 || N <= 0 || K <= 0 || (M <= 16 && !forced)) return p;
-  if (std::getenv("MTP_WS_TUNE") && *std::getenv("MTP_WS_TUNE")) return p;  // sweeps of wsp
+  if (tune(kTuneWsVariant) >= 0 || tune(kTuneWsSplits) > 0) return p;  // sweeps of wsp
   const int wb = dtype_bytes(wt);
   if ((K * wb) % kSkUB != 0 || K > 256 * 8 * kSkPrepChunks) return p;
   // buffer descriptors: the workgroup's W rows, all xn blocks
@@ -351,9 +398,9 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   p.nkb = (int)(K * wb / kSkUB);
   int S = 1;
   if (forced) {
-    S = std::max(1, std::atoi(force));
+    S = force;
   } else {
-    while ((int64_t)p.G * S < kSkMinBlocks && p.nkb / (S + 1) >= kSkMinStages) ++S;
+    while ((int64_t)p.G * S < sk_min_blocks() && p.nkb / (S + 1) >= kSkMinStages) ++S;
   }
   if (S > p.nkb) S = p.nkb;
   p.kb_per = (p.nkb + S - 1) / S;
@@ -417,7 +464,6 @@ struct PlanSkl {
   size_t part_off = 0, ss_off = 0, total = 0;
 };
 
-constexpr int kSklCUs = 256;  // compute units of the device (one workgroup each)
 
 // MTP_SKL=1 forces the single-launch kernel wherever it applies, MTP_SKL=0
 // turns it off. By default it runs where its 256-column tiles fill the CUs
@@ -430,11 +476,7 @@ constexpr int kSklCUs = 256;  // compute units of the device (one workgroup each
 // 14336 18.6 vs 21.5, M 8 N 8192 17.8 vs 14.5 (below the bound), bf16 M 16
 // N 28672 51.4 vs 72.1; fp8 M 64 N 14336 (four splits) 27.8 us vs 25.7 us.
 constexpr int64_t kSklSplitMinWBytes = (int64_t)48 << 20;
-int skl_mode() {
-  const char *e = std::getenv("MTP_SKL");
-  if (!e || !*e) return -1;
-  return *e == '0' ? 0 : 1;
-}
+int skl_mode() { return tune(kTuneSkl); }
 
 PlanSkl make_plan_skl(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   PlanSkl p;
@@ -446,8 +488,7 @@ PlanSkl make_plan_skl(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
   if (M <= 0 || M > 64 || N <= 0 || K <= 0) return p;
   const int wb = dtype_bytes(wt);
   if ((K * wb) % kSkUB != 0) return p;
-  const char *nwe = std::getenv("MTP_SKL_WAVES");
-  if (nwe && *nwe) p.nw = std::atoi(nwe) == 4 ? 4 : 8;
+  if (tune(kTuneSklWaves) > 0) p.nw = tune(kTuneSklWaves) == 4 ? 4 : 8;
   const int64_t bn = skl_bn(p.nw);
   // buffer descriptors: x, the workgroup's W rows (32-bit sizes and offsets)
   if (M * K * 2 >= ((int64_t)1 << 31) || bn * K * wb >= ((int64_t)1 << 31)) return p;
@@ -456,9 +497,8 @@ PlanSkl make_plan_skl(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
   p.nkb = (int)(K * wb / kSkUB);
   const int uk = kSkUB / wb;  // k per stage
   int S = 1;
-  const char *force = std::getenv("MTP_SKL_SPLITS");
-  if (force && *force) S = std::max(1, std::atoi(force));
-  else S = std::max(1, kSklCUs / std::max(1, p.G));
+  if (tune(kTuneSklSplits) > 0) S = tune(kTuneSklSplits);
+  else S = std::max(1, device_cus() / std::max(1, p.G));
   if (S > p.nkb) S = p.nkb;
   for (;;) {
     p.kb_per = (p.nkb + S - 1) / S;
@@ -602,7 +642,8 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
 
 // ---------------------------------------------------------------------------
 // Attention: plan and launch.
-constexpr int kAttnTargetBlocks = 256;  // 8-wave workgroups that fill the chip once
+// 8-wave workgroups that fill the chip once: one per CU
+int attn_target_blocks() { return device_cus(); }
 
 struct AttnPlan {
   int qt = 0, nchunks = 1, chunk_blocks = 0;
@@ -612,8 +653,8 @@ struct AttnPlan {
 
 // Key blocks of kAttnBlock (context, then dense) are split into chunks of
 // chunk_blocks consecutive blocks, one workgroup each, so that the launch
-// has at most kAttnTargetBlocks workgroups (one per CU) where the heads
-// allow; MTP_ATTN_CHUNK_BLOCKS overrides the chunk length.
+// has at most one workgroup per CU where the heads allow; the
+// attn_chunk_blocks tuning key overrides the chunk length.
 AttnPlan make_attn_plan(int ct, int64_t B, int64_t NQ, int64_t H, int64_t D, int64_t Lc,
                         int64_t Lt) {
   AttnPlan p;
@@ -622,9 +663,9 @@ AttnPlan make_attn_plan(int ct, int64_t B, int64_t NQ, int64_t H, int64_t D, int
   p.qt = (int)((NQ + 15) / 16);
   const int64_t ntot = (Lc + kAttnBlock - 1) / kAttnBlock + (Lt + kAttnBlock - 1) / kAttnBlock;
   if (ntot == 0) return p;
-  const int64_t want = std::max<int64_t>(1, kAttnTargetBlocks / (B * H));
+  const int64_t want = std::max<int64_t>(1, attn_target_blocks() / (B * H));
   int64_t cb = (ntot + want - 1) / want;
-  if (const char *e = getenv("MTP_ATTN_CHUNK_BLOCKS")) cb = std::max<int64_t>(1, atoll(e));
+  if (tune(kTuneAttnChunkBlocks) > 0) cb = tune(kTuneAttnChunkBlocks);
   cb = std::max(cb, (ntot + kAttnMaxChunks - 1) / kAttnMaxChunks);
   p.chunk_blocks = (int)std::min<int64_t>(cb, ntot);
   p.nchunks = (int)((ntot + p.chunk_blocks - 1) / p.chunk_blocks);
@@ -651,7 +692,7 @@ int launch_attention(AttnArgs &a, int ct, int64_t D, void *ws, size_t ws_bytes, 
   const bool aligned = aligned16(a.q) && aligned16(a.out) && (!a.kp || aligned16(a.kp)) &&
                        (!a.vp || aligned16(a.vp)) && (!a.kd || aligned16(a.kd)) &&
                        (!a.vd || aligned16(a.vd));
-  if (p.fast && strides8 && aligned) {
+  if (p.fast && strides8 && aligned && !a.kv_fp8) {
     if (p.total > 0 && (!ws || ws_bytes < p.total)) return MTP_ERR_WORKSPACE;
     AttnKernel k = attn_pick(ct, (int)D);
     AttnKernel km = attn_merge_pick(ct, (int)D);
@@ -732,7 +773,7 @@ int launch_int4(const void *x, int xdt, int64_t M, int64_t K, const uint8_t *pac
   // K 8192, N 28672 137 us against 143 us with 4; MTP_INT4_WAVES=4|8
   // overrides (tuning)
   int nw = tl.mt == 4 ? 8 : 4;
-  if (const char *e = std::getenv("MTP_INT4_WAVES")) nw = std::atoi(e) == 8 ? 8 : 4;
+  if (tune(kTuneInt4Waves) > 0) nw = tune(kTuneInt4Waves) == 8 ? 8 : 4;
   I4Kernel gemm = int4_gemm_pick(tl.mt, tl.na, nw, nibble == MTP_NIBBLE_TWOS);
   if (!gemm) return MTP_ERR_DTYPE;
   const int64_t gn = (N + 128 * tl.na - 1) / (128 * tl.na);
@@ -792,6 +833,30 @@ const char *mtp_status_string(int status) {
 }
 
 const char *mtp_last_hip_error(void) { return g_last_hip_error; }
+
+int mtp_set_tuning(const char *name, int64_t value) {
+  if (!name) return MTP_ERR_NULL;
+  tune(kTuneSkl);  // the environment seeds the keys first
+  for (int k = 0; k < kTuneCount; ++k) {
+    if (std::strcmp(name, kTuneNames[k]) == 0) {
+      if (value < -1 || value > INT32_MAX) return MTP_ERR_ARG;
+      g_tune[k].store((int)value, std::memory_order_relaxed);
+      return MTP_OK;
+    }
+  }
+  return MTP_ERR_ARG;
+}
+
+int mtp_get_tuning(const char *name, int64_t *value) {
+  if (!name || !value) return MTP_ERR_NULL;
+  for (int k = 0; k < kTuneCount; ++k) {
+    if (std::strcmp(name, kTuneNames[k]) == 0) {
+      *value = tune((TuneKey)k);
+      return MTP_OK;
+    }
+  }
+  return MTP_ERR_ARG;
+}
 
 size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, int64_t N,
                                           int64_t K) {
@@ -858,24 +923,23 @@ int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K, cons
 static int verify_rows_per_chunk(int64_t seq) { return (int)((64 / seq) * seq); }
 
 // Persistent streaming verify (skv.hpp): 16-bit hidden and weights, no bias,
-// K a multiple of 512 (whole rounds of the 8-stage ring per tile), W within
-// the 2 GiB reach of one buffer descriptor. MTP_VERIFY_WSTREAM selects the
-// column-group kernel instead.
-constexpr size_t kSkvKeysBytes = 64 * 8;
+// K a multiple of 256 (the stages of a tile, 64 k each, are whole rounds of
+// the 4-slot register ring), W within the 2 GiB reach of one buffer
+// descriptor. MTP_VERIFY_WSTREAM selects the column-group kernel instead.
 bool skv_usable(int ht, int64_t V, int64_t K, const void *bias) {
   if (ht != MTP_BF16 && ht != MTP_F16) return false;
-  if (bias || K <= 0 || K % 512 != 0 || V <= 0) return false;
+  if (bias || K <= 0 || K % 256 != 0 || V <= 0) return false;
   if (V * K * 2 >= ((int64_t)1 << 31)) return false;
-  const char *e = std::getenv("MTP_VERIFY_WSTREAM");
-  return !(e && *e);
+  return tune(kTuneVerifyWstream) <= 0;
 }
 
 size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq, int64_t V, int64_t K) {
   if (seq < 1 || seq > 64) return 0;
   Plan p = make_plan(h_dtype, h_dtype, rows, V, K, EPI_ARGMAX, verify_rows_per_chunk(seq));
+  // the persistent and generic kernels need the counter prefix (keys and
+  // ticket); the column-group kernel its per-tile maxima after it
   const size_t wsb = p.generic ? 0 : p.total;
-  const size_t skv = (h_dtype == MTP_BF16 || h_dtype == MTP_F16) ? kCounterBytes + kSkvKeysBytes : 0;
-  return std::max(wsb, skv);
+  return std::max(wsb, kCounterBytes);
 }
 
 // One launch per chunk of rows_per_chunk rows (whole batch elements).
@@ -883,10 +947,10 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
                       int rows_per_chunk, const WsArgs &o, void *ws, size_t ws_bytes,
                       hipStream_t st) {
   if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;
-  if (!ws || ws_bytes < kCounterBytes + kSkvKeysBytes) return MTP_ERR_WORKSPACE;
+  if (!ws || ws_bytes < kCounterBytes) return MTP_ERR_WORKSPACE;
   unsigned char *w8 = (unsigned char *)ws;
   const int64_t ntiles = (V + kSkvBN - 1) / kSkvBN;
-  const int grid = (int)std::min<int64_t>(ntiles, kSkvBlocks);
+  const int grid = (int)std::min<int64_t>(ntiles, device_cus());
   for (int64_t m0 = 0; m0 < rows; m0 += rows_per_chunk) {
     const int Mloc = (int)std::min<int64_t>(rows_per_chunk, rows - m0);
     SkvKernel k = skv_pick(ht, Mloc <= 32 ? 1 : 2);
@@ -899,7 +963,7 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
     a.K = (int)K;
     a.ntiles = (int)ntiles;
     a.nst = (int)(K / 64);
-    a.keys = (unsigned long long *)(w8 + kCounterBytes);
+    a.keys = (unsigned long long *)(w8 + kSkvKeysOff);
     a.ticket = (unsigned *)w8;
     a.multi = o.multi;
     if (!o.multi) {
@@ -922,15 +986,66 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
   return MTP_OK;
 }
 
+// Generic verify (vgen.hpp): any K, alignment and float dtypes; one launch
+// per chunk of rows_per_chunk rows (whole batch elements).
+constexpr int kVgenMaxBlocks = 1024;
+static int launch_vgen(const void *hidden, int ht, int64_t rows, int64_t K, const void *w, int wt,
+                       int64_t V, const void *bias, int bt, int rows_per_chunk, const WsArgs &o,
+                       void *ws, size_t ws_bytes, hipStream_t st) {
+  if (!ws || ws_bytes < kCounterBytes) return MTP_ERR_WORKSPACE;
+  unsigned char *w8 = (unsigned char *)ws;
+  const int grid = (int)std::min<int64_t>((V + kVgenThreads - 1) / kVgenThreads, kVgenMaxBlocks);
+  for (int64_t m0 = 0; m0 < rows; m0 += rows_per_chunk) {
+    const int Mloc = (int)std::min<int64_t>(rows_per_chunk, rows - m0);
+    VgenKernel k = vgen_pick(Mloc);
+    if (!k) return MTP_ERR_SHAPE;
+    VgenArgs a{};
+    a.x = (const unsigned char *)hidden + m0 * K * dtype_bytes(ht);
+    a.xdt = ht;
+    a.w = w;
+    a.wdt = wt;
+    a.bias = bias;
+    a.bdt = bt;
+    a.M = Mloc;
+    a.N = (int)V;
+    a.K = (int)K;
+    a.keys = (unsigned long long *)(w8 + kSkvKeysOff);
+    a.ticket = (unsigned *)w8;
+    a.out.multi = o.multi;
+    if (!o.multi) {
+      a.out.draft = o.draft + m0;
+      a.out.accept = o.accept + m0;
+    } else {
+      const int64_t b0 = m0 / o.S_seq;
+      a.out.S_seq = o.S_seq;
+      a.out.D = o.D;
+      a.out.draft = o.draft ? o.draft + b0 * o.D : nullptr;
+      a.out.accept = o.accept ? o.accept + b0 * o.D : nullptr;
+      a.out.accepted_n = o.accepted_n + b0;
+      a.out.corrected = o.corrected + b0;
+    }
+    a.out.top = o.top ? o.top + m0 : nullptr;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kVgenThreads), 0, st, a);
+    const int s = launch_status();
+    if (s != MTP_OK) return s;
+  }
+  return MTP_OK;
+}
+
+// Route: the persistent streaming kernel (16-bit, no bias, K % 256 == 0,
+// 16-byte aligned), else the column-group streaming kernel (same dtype for
+// hidden and W, 16-byte rows and pointers), else the generic kernel.
 static int verify_common(const void *hidden, int ht, int64_t rows, int64_t K, const void *w,
                          int wt, int64_t V, const void *bias, int bt, int rows_per_chunk,
                          WsArgs &a, void *ws, size_t ws_bytes, void *stream) {
-  if (skv_usable(ht, V, K, bias))
+  const bool aligned = aligned16(hidden) && aligned16(w);
+  if (wt == ht && aligned && skv_usable(ht, V, K, bias))
     return launch_skv(hidden, ht, rows, K, w, V, rows_per_chunk, a, ws, ws_bytes,
                       (hipStream_t)stream);
   Plan p = make_plan(ht, wt, rows, V, K, EPI_ARGMAX, rows_per_chunk);
-  if (p.generic) return MTP_ERR_SHAPE;
-  if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;
+  if (p.generic || !aligned || wt != ht || (bias && !aligned16(bias)))
+    return launch_vgen(hidden, ht, rows, K, w, wt, V, bias, bt, rows_per_chunk, a, ws, ws_bytes,
+                       (hipStream_t)stream);
   if (!ws || ws_bytes < p.total) return MTP_ERR_WORKSPACE;
   a.x = hidden;
   a.w = w;
@@ -947,7 +1062,7 @@ int mtp_fused_verify(const void *hidden, int h_dtype, int64_t M, int64_t K, cons
                      int w_dtype, int64_t V, const void *bias, int bias_dtype,
                      const int32_t *draft, int8_t *accept, int32_t *top, void *workspace,
                      size_t workspace_bytes, void *stream) {
-  if (!is_float_dt(h_dtype) || w_dtype != h_dtype) return MTP_ERR_DTYPE;
+  if (!is_float_dt(h_dtype) || !is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
   if (bias && !is_float_dt(bias_dtype)) return MTP_ERR_DTYPE;
   if (M < 0 || K <= 0 || V <= 0 || M > INT32_MAX || K > INT32_MAX || V > INT32_MAX)
     return MTP_ERR_SHAPE;
@@ -967,7 +1082,7 @@ int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B, int64_t S
                            int bias_dtype, const int32_t *draft, int64_t D, int8_t *accept,
                            int32_t *accepted_n, int32_t *corrected, int32_t *top_out,
                            void *workspace, size_t workspace_bytes, void *stream) {
-  if (!is_float_dt(h_dtype) || w_dtype != h_dtype) return MTP_ERR_DTYPE;
+  if (!is_float_dt(h_dtype) || !is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
   if (bias && !is_float_dt(bias_dtype)) return MTP_ERR_DTYPE;
   if (B < 0 || S < 1 || D < 0 || S != D + 1 || K <= 0 || V <= 0 || S > 64 ||
       B * S > INT32_MAX || K > INT32_MAX || V > INT32_MAX)
@@ -1034,15 +1149,18 @@ int mtp_fused_paged_attention(const void *q, int dtype, int64_t B, int64_t H, in
   return launch_attention(a, dtype, D, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-int mtp_fused_tree_attention(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
-                             const void *k, const void *v, int64_t L, const void *mask,
-                             int mask_dtype, float scale, void *out, void *workspace,
-                             size_t workspace_bytes, void *stream) {
+// Single-query attention over dense keys k / v [B, H, L, D] (element type
+// dtype, or fp8 with per-head scales), optional 1-D mask [L].
+static int dense_attention(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                           const void *k, const void *v, int64_t L, const void *mask,
+                           int mask_dtype, int kv_fp8, const float *kscale, const float *vscale,
+                           float scale, void *out, void *workspace, size_t workspace_bytes,
+                           void *stream) {
   if (!is_float_dt(dtype)) return MTP_ERR_DTYPE;
   if (mask && !mask_dt_ok(mask_dtype)) return MTP_ERR_DTYPE;
   if (B < 0 || H < 0 || D <= 0 || L < 0 || L > INT32_MAX) return MTP_ERR_SHAPE;
   if (B == 0 || H == 0) return MTP_OK;
-  if (!q || !out || (L > 0 && (!k || !v || !mask))) return MTP_ERR_NULL;
+  if (!q || !out || (L > 0 && (!k || !v))) return MTP_ERR_NULL;
   AttnArgs a{};
   a.q = q;
   a.q_sb = H * D;
@@ -1063,7 +1181,81 @@ int mtp_fused_tree_attention(const void *q, int dtype, int64_t B, int64_t H, int
   a.NQ = 1;
   a.H = (int)H;
   a.scale = scale;
+  a.kv_fp8 = kv_fp8;
+  a.kscale = kscale;
+  a.vscale = vscale;
   return launch_attention(a, dtype, D, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mtp_fused_tree_attention(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                             const void *k, const void *v, int64_t L, const void *mask,
+                             int mask_dtype, float scale, void *out, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  if (L > 0 && B > 0 && H > 0 && !mask) return MTP_ERR_NULL;
+  return dense_attention(q, dtype, B, H, D, k, v, L, mask, mask_dtype, 0, nullptr, nullptr, scale,
+                         out, workspace, workspace_bytes, stream);
+}
+
+int mtp_fused_causal_attention(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                               const void *k, const void *v, int64_t L, float scale, void *out,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  return dense_attention(q, dtype, B, H, D, k, v, L, nullptr, 0, 0, nullptr, nullptr, scale, out,
+                         workspace, workspace_bytes, stream);
+}
+
+int mtp_fused_causal_attention_fp8(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                                   const void *k_fp8, const void *v_fp8, int64_t L,
+                                   const float *kscale, const float *vscale, float scale,
+                                   void *out, void *stream) {
+  if (B > 0 && H > 0 && (!kscale || !vscale)) return MTP_ERR_NULL;
+  // the fp8 fallback kernel needs no workspace
+  return dense_attention(q, dtype, B, H, D, k_fp8, v_fp8, L, nullptr, 0, 1, kscale, vscale, scale,
+                         out, nullptr, 0, stream);
+}
+
+// Tree monolith: attention over the masked keys into an intermediate
+// [B * H, D] (q's dtype) at the end of the workspace, then RMSNorm over the
+// head dimension (gamma rms_w) and the projection onto proj_w's rows.
+static size_t monolith_tmp_off(int dtype, int64_t B, int64_t H, int64_t D, int64_t L, int w_kind,
+                               int64_t N) {
+  const size_t att = make_attn_plan(dtype, B, 1, H, D, 0, L).total;
+  const size_t lin = mtp_rmsnorm_linear_workspace_bytes(dtype, w_kind, B * H, N, D);
+  return align_up(std::max(kCounterBytes, std::max(att, lin)), 256);
+}
+
+size_t mtp_tree_attn_rmsnorm_linear_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t D,
+                                                    int64_t L, int w_kind, int64_t N) {
+  if (B <= 0 || H <= 0 || D <= 0 || L < 0 || N <= 0) return 0;
+  return monolith_tmp_off(dtype, B, H, D, L, w_kind, N) +
+         align_up((size_t)(B * H * D) * dtype_bytes(dtype), 256);
+}
+
+int mtp_fused_tree_attn_rmsnorm_linear(const void *q, int dtype, int64_t B, int64_t H, int64_t D,
+                                       const void *k, const void *v, int64_t L, const void *mask,
+                                       int mask_dtype, const void *proj_w, int w_dtype, int64_t N,
+                                       const void *rms_w, int rms_dtype, const void *proj_bias,
+                                       int bias_dtype, const float *wscale, float scale, float eps,
+                                       void *out, void *workspace, size_t workspace_bytes,
+                                       void *stream) {
+  if (!is_float_dt(dtype) || !mask_dt_ok(mask_dtype)) return MTP_ERR_DTYPE;
+  if (!(is_float_dt(w_dtype) || w_dtype == MTP_FP8E4M3)) return MTP_ERR_DTYPE;
+  if (w_dtype == MTP_FP8E4M3 && !wscale) return MTP_ERR_NULL;
+  if (B < 0 || H < 0 || D <= 0 || L < 0 || N < 0 || L > INT32_MAX || N > INT32_MAX ||
+      B * H > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  if (B == 0 || H == 0 || N == 0) return MTP_OK;
+  if (!q || !out || !proj_w || (L > 0 && (!k || !v || !mask))) return MTP_ERR_NULL;
+  const size_t need = mtp_tree_attn_rmsnorm_linear_workspace_bytes(dtype, B, H, D, L,
+                                                                   wscale ? MTP_FP8E4M3 : w_dtype, N);
+  if (!workspace || workspace_bytes < need) return MTP_ERR_WORKSPACE;
+  const size_t off = monolith_tmp_off(dtype, B, H, D, L, wscale ? MTP_FP8E4M3 : w_dtype, N);
+  void *tmp = (unsigned char *)workspace + off;
+  int s = dense_attention(q, dtype, B, H, D, k, v, L, mask, mask_dtype, 0, nullptr, nullptr, scale,
+                          tmp, workspace, off, stream);
+  if (s != MTP_OK) return s;
+  return rmsnorm_linear_impl(tmp, dtype, B * H, D, proj_w, w_dtype, N, wscale, proj_bias,
+                             bias_dtype, rms_w, rms_dtype, eps, 1.0f, 1, out, workspace, off,
+                             stream);
 }
 
 int mtp_tree_verify_attention(const void *q_nodes, int dtype, int64_t N, int64_t H, int64_t D,

@@ -5,7 +5,7 @@
 //   top[m] = argmax_n (x[m] . W[n])   (torch.argmax: NaN is the maximum,
 //                                      the lowest index wins ties)
 //
-// One launch of kSkvBlocks workgroups (one per CU) streams W once.
+// One launch of one workgroup per CU streams W once.
 // Workgroup b takes the kSkvBN-column tiles b, b + grid, b + 2 grid, ...
 // back to back; the stages (64 k = 128 bytes of every W row of a tile) of
 // all its tiles form one sequence, so the register rings run across tile
@@ -32,20 +32,9 @@
 
 #include "sk.hpp"
 #include "skv_args.hpp"
+#include "verify_tail.hpp"
 
 namespace mtp {
-
-// (value, column) -> key; unsigned key order == torch.argmax preference.
-__device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
-  uint32_t b = __float_as_uint(v);
-  if (v != v) b = 0x7fc00000u;  // every NaN alike: above +inf
-  else if (v == 0.f) b = 0u;    // -0 == +0
-  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
-}
-__device__ __forceinline__ int argmax_key_index(unsigned long long k) {
-  return (int)(0xffffffffu - (uint32_t)k);
-}
 
 template <int CT, int MT>
 __global__ void __launch_bounds__(512, 1)
@@ -236,46 +225,24 @@ skv_kernel(const SkvArgs a) {
     unsigned long long k = s_key[0][th];
 #pragma unroll
     for (int w = 1; w < 8; ++w) k = s_key[w][th] > k ? s_key[w][th] : k;
-    if (k != 0ull)
-      __hip_atomic_fetch_max(a.keys + th, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    key_max(a.keys, th, k);
   }
   wait_stores();
   __syncthreads();
   if (th == 0) s_flag = ticket_add(a.ticket) == (unsigned)(grid - 1);
   __syncthreads();
   if (!s_flag) return;
-  // the drafts (fewer than the rows) go to LDS with the same round trip as
-  // the row keys; read in the acceptance chain, they would be re-read from
-  // memory after every accept store (byte stores may alias them)
-  {
-    const int nd = a.multi ? a.M / a.S_seq * a.D : a.M;
-    if (th < nd && a.draft) s_draft[th] = a.draft[th];
-  }
-  for (int m = th; m < a.M; m += 512) {
-    const unsigned long long k =
-        __hip_atomic_load(a.keys + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_top[m] = argmax_key_index(k);
-    __hip_atomic_store(a.keys + m, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (a.top)
-    for (int m = th; m < a.M; m += 512) a.top[m] = s_top[m];
-  if (!a.multi) {
-    for (int m = th; m < a.M; m += 512) a.accept[m] = (int8_t)(s_top[m] == s_draft[m]);
-  } else {
-    const int Sq = a.S_seq, Dd = a.D;
-    for (int bl = th; bl < a.M / Sq; bl += 512) {
-      const int *tp = s_top + bl * Sq;
-      a.corrected[bl] = tp[0];
-      int n = 0;
-      for (int d = 0; d < Dd; ++d) {
-        const bool ok = (tp[d + 1] == s_draft[bl * Dd + d]) && (n == d);
-        a.accept[(int64_t)bl * Dd + d] = (int8_t)ok;
-        if (ok) n = d + 1;
-      }
-      a.accepted_n[bl] = n;
-    }
-  }
+  handoff_acquire();
+  VerifyOut o;
+  o.draft = a.draft;
+  o.accept = a.accept;
+  o.accepted_n = a.accepted_n;
+  o.corrected = a.corrected;
+  o.top = a.top;
+  o.S_seq = a.S_seq;
+  o.D = a.D;
+  o.multi = a.multi;
+  verify_finish(a.keys, a.M, o, s_top, s_draft);
   if (th == 0) ticket_reset(a.ticket);
 }
 

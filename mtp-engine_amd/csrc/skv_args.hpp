@@ -7,7 +7,6 @@
 
 namespace mtp {
 
-constexpr int kSkvBlocks = 256;  // persistent workgroups: one per CU
 constexpr int kSkvBN = 256;      // columns per tile
 
 struct SkvArgs {

@@ -67,6 +67,28 @@ SIGNATURES = {
     "mtp_dequantize_fp8": (_i, [_vp, _i64, _i64, _vp, _i, _vp, _vp]),
     "mtp_quantize_int4": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _vp]),
     "mtp_dequantize_int4": (_i, [_vp, _vp, _i, _i64, _i64, _i64, _vp, _vp]),
+    "mtp_fused_causal_attention": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _f, _vp, _vp, _sz, _vp]),
+    "mtp_fused_causal_attention_fp8": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _f, _vp, _vp]),
+    "mtp_fused_tree_attn_rmsnorm_linear": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i, _vp, _i, _i64, _vp, _i, _vp, _i,
+             _vp, _f, _f, _vp, _vp, _sz, _vp]),
+    "mtp_tree_attn_rmsnorm_linear_workspace_bytes": (_sz, [_i, _i64, _i64, _i64, _i64, _i, _i64]),
+    "mtp_fused_rmsnorm": (_i, [_vp, _i, _i64, _i64, _vp, _i, _f, _vp, _vp]),
+    "mtp_fused_add_rmsnorm": (_i, [_vp, _vp, _i, _i64, _i64, _vp, _i, _f, _vp, _vp]),
+    "mtp_argmax": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "mtp_argmax_workspace_bytes": (_sz, [_i64, _i64]),
+    "mtp_paged_kv_write": (
+        _i, [_vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i, _i64, _i64,
+             _vp, _i64, _vp, _i, _i64, _vp]),
+    "mtp_verify_commit": (
+        _i, [_vp, _vp, _vp, _vp, _i, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "mtp_batch_prefix_match": (_i, [_vp, _i64, _i64, _vp, _vp]),
+    "mtp_workspace_init": (_i, [_vp, _sz, _vp]),
+    "mtp_set_tuning": (_i, [ctypes.c_char_p, _i64]),
+    "mtp_get_tuning": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lib = None
@@ -118,6 +140,40 @@ def check(status: int, what: str) -> None:
     raise MtpHipError(f"{what}: {msg} (status {status})")
 
 
+# Launch-planning overrides of the library (mtp_set_tuning): -1 = the plan's.
+TUNING_KEYS = ("skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
+               "attn_chunk_blocks", "int4_waves", "verify_wstream")
+
+
+def set_tuning(**keys: int) -> None:
+    lib = load()
+    for k, v in keys.items():
+        check(lib.mtp_set_tuning(k.encode(), int(v)), f"set_tuning({k})")
+
+
+def get_tuning(name: str) -> int:
+    v = ctypes.c_int64(0)
+    check(load().mtp_get_tuning(name.encode(), ctypes.byref(v)), f"get_tuning({name})")
+    return int(v.value)
+
+
+class tuning:
+    """Context manager: set tuning keys, restore the previous values on exit."""
+
+    def __init__(self, **keys: int):
+        self.keys = keys
+        self.old = {}
+
+    def __enter__(self):
+        self.old = {k: get_tuning(k) for k in self.keys}
+        set_tuning(**self.keys)
+        return self
+
+    def __exit__(self, *exc):
+        set_tuning(**self.old)
+        return False
+
+
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -127,9 +183,21 @@ def stream_handle(device: torch.device) -> int:
 
 
 # ---------------------------------------------------------------------------
-# Workspace: one zero-initialised buffer per (device, stream), grown on
-# demand. Kernels leave their counters at zero, so the buffer is reused as is.
+# Workspace: one buffer per (device, stream), grown on demand and zeroed by
+# the library's own fill kernel (so a buffer created while a stream is being
+# captured records a kernel node, not a memset). Kernels leave their counters
+# at zero, so the buffer is reused as is. reserve_workspace() sizes it ahead
+# of a graph capture, so the capture allocates nothing.
 _workspaces: dict = {}
+_MIN_WORKSPACE = MTP_COUNTER_BYTES = 65536
+
+
+def _new_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    nbytes = (nbytes + 255) // 256 * 256
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    check(load().mtp_workspace_init(ws.data_ptr(), nbytes, stream_handle(device)),
+          "workspace init")
+    return ws
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -138,7 +206,16 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, 0 if ws is None else 2 * ws.numel())
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        size = max(nbytes, _MIN_WORKSPACE, 0 if ws is None else 2 * ws.numel())
+        ws = _new_workspace(device, size)
         _workspaces[key] = ws
     return ws
+
+
+def reserve_workspace(device: torch.device, nbytes: int, stream=None) -> torch.Tensor:
+    """Make the workspace of (device, stream) at least nbytes now (default:
+    the current stream), e.g. before capturing calls on that stream."""
+    device = torch.device(device)
+    st = stream if stream is not None else torch.cuda.current_stream(device)
+    with torch.cuda.stream(st):
+        return workspace(device, max(int(nbytes), _MIN_WORKSPACE))

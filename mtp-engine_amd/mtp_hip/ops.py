@@ -382,3 +382,260 @@ def dequantize_int4(packed: torch.Tensor, scales: torch.Tensor, K: int, group: i
                                  ptr(out), _lib.stream_handle(packed.device))
     check(st, "dequantize_int4")
     return out
+
+
+# ---------------------------------------------------------------------------
+# Draft chain
+def rmsnorm(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+            residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """(x [+ residual]) * rsqrt(mean(.^2) + eps) * weight over the last dim of
+    a 2-D x, in x.dtype. The weight is cast to x.dtype first, as the
+    reference's wrappers do (mtp_kernels.py:918-920, 1088-1090)."""
+    lib = _lib.load()
+    x = x.contiguous()
+    assert x.dim() == 2, "fused_rmsnorm: x must be 2-D [M, N]"
+    M, N = x.shape
+    if weight is not None:
+        weight = weight.contiguous().to(dtype=x.dtype, device=x.device)
+        assert weight.numel() == N, f"fused_rmsnorm: weight has {weight.numel()} != {N}"
+    if residual is not None:
+        residual = residual.contiguous()
+        assert residual.shape == x.shape, "fused_add_rmsnorm: residual shape differs from x"
+        if residual.dtype != x.dtype:
+            residual = residual.to(x.dtype)
+    _on_device("x", x, weight=weight, residual=residual)
+    y = torch.empty_like(x)
+    wcode = code(weight.dtype) if weight is not None else 0
+    st = _lib.stream_handle(x.device)
+    if residual is None:
+        s = lib.mtp_fused_rmsnorm(ptr(x), code(x.dtype), M, N, ptr(weight), wcode, float(eps),
+                                  ptr(y), st)
+        check(s, "fused_rmsnorm")
+    else:
+        s = lib.mtp_fused_add_rmsnorm(ptr(x), ptr(residual), code(x.dtype), M, N, ptr(weight),
+                                      wcode, float(eps), ptr(y), st)
+        check(s, "fused_add_rmsnorm")
+    return y
+
+
+def argmax(logits: torch.Tensor, emb_table: Optional[torch.Tensor] = None):
+    """torch.argmax(logits, dim=-1) (int64; NaN is the maximum, the lowest
+    index wins ties) over a 2-D (or 1-D) float tensor; with emb_table
+    [V', H] also returns emb_table[tokens] from the same launch."""
+    lib = _lib.load()
+    one_d = logits.dim() == 1
+    lg = logits.reshape(1, -1) if one_d else logits
+    assert lg.dim() == 2, "argmax: logits must be 1-D or 2-D"
+    if lg.stride(-1) != 1:
+        lg = lg.contiguous()
+    M, V = lg.shape
+    ld = lg.stride(0) if M > 1 else V
+    _on_device("logits", lg, emb_table=emb_table)
+    tokens = torch.empty((M,), dtype=torch.int64, device=lg.device)
+    emb = None
+    if emb_table is not None:
+        emb_table = emb_table.contiguous()
+        assert emb_table.dim() == 2, "argmax: emb_table must be [V, H]"
+        emb = torch.empty((M, emb_table.shape[1]), dtype=emb_table.dtype, device=lg.device)
+    nbytes = lib.mtp_argmax_workspace_bytes(M, V)
+    ws = _lib.workspace(lg.device, nbytes)
+    s = lib.mtp_argmax(ptr(lg), code(lg.dtype), M, V, ld, ptr(tokens), ptr(emb_table),
+                       code(emb_table.dtype) if emb_table is not None else 0,
+                       emb_table.shape[0] if emb_table is not None else 0,
+                       emb_table.shape[1] if emb_table is not None else 0, ptr(emb), ptr(ws),
+                       nbytes, _lib.stream_handle(lg.device))
+    check(s, "argmax")
+    if one_d:
+        tokens = tokens.reshape(())
+        emb = emb.reshape(-1) if emb is not None else None
+    return tokens if emb_table is None else (tokens, emb)
+
+
+# ---------------------------------------------------------------------------
+# Decode attention and the tree monolith
+def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     scale: Optional[float] = None) -> torch.Tensor:
+    """out[b, h] = softmax_l(q . k_l * scale) @ v_l (a single query that
+    attends every key): q [B, H, D], k / v [B, H, L, D]."""
+    lib = _lib.load()
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    B, H, D = q.shape
+    _B, _H, L, _D = k.shape
+    assert B == _B and H == _H and D == _D
+    assert v.shape == k.shape and k.dtype == q.dtype and v.dtype == q.dtype, \
+        "fused_causal_attention: k / v shape or dtype differs"
+    _on_device("q", q, k=k, v=v)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty_like(q)
+    nbytes = lib.mtp_attention_workspace_bytes(code(q.dtype), B, 1, H, D, 0, L)
+    ws = _lib.workspace(q.device, nbytes)
+    s = lib.mtp_fused_causal_attention(ptr(q), code(q.dtype), B, H, D, ptr(k), ptr(v), L,
+                                       float(scale), ptr(out), ptr(ws), nbytes,
+                                       _lib.stream_handle(q.device))
+    check(s, "fused_causal_attention")
+    return out
+
+
+def causal_attention_fp8(q: torch.Tensor, k_fp8: torch.Tensor, v_fp8: torch.Tensor,
+                         kscale: torch.Tensor, vscale: torch.Tensor,
+                         scale: Optional[float] = None) -> torch.Tensor:
+    """causal_attention with fp8 e4m3fn K / V dequantised per head by kscale
+    [H] / vscale [H]."""
+    lib = _lib.load()
+    q, k_fp8, v_fp8 = q.contiguous(), k_fp8.contiguous(), v_fp8.contiguous()
+    kscale = kscale.contiguous().to(torch.float32)
+    vscale = vscale.contiguous().to(torch.float32)
+    B, H, D = q.shape
+    _B, _H, L, _D = k_fp8.shape
+    assert (B, H, D) == (_B, _H, _D)
+    assert v_fp8.shape == k_fp8.shape, "fused_causal_attention_fp8: v shape differs from k"
+    assert k_fp8.dtype == torch.float8_e4m3fn and v_fp8.dtype == torch.float8_e4m3fn, \
+        "fused_causal_attention_fp8: k / v must be float8_e4m3fn"
+    assert kscale.numel() == H and vscale.numel() == H, "fused_causal_attention_fp8: scales [H]"
+    _on_device("q", q, k_fp8=k_fp8, v_fp8=v_fp8, kscale=kscale, vscale=vscale)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty_like(q)
+    s = lib.mtp_fused_causal_attention_fp8(ptr(q), code(q.dtype), B, H, D, ptr(k_fp8),
+                                           ptr(v_fp8), L, ptr(kscale), ptr(vscale), float(scale),
+                                           ptr(out), _lib.stream_handle(q.device))
+    check(s, "fused_causal_attention_fp8")
+    return out
+
+
+def tree_attn_rmsnorm_linear(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             mask: torch.Tensor, proj_w: torch.Tensor,
+                             rms_w: Optional[torch.Tensor] = None,
+                             proj_bias: Optional[torch.Tensor] = None,
+                             wscale: Optional[torch.Tensor] = None,
+                             scale: Optional[float] = None, eps: float = 1e-6) -> torch.Tensor:
+    """Masked single-query attention, RMSNorm over the head dim (gamma
+    rms_w), projection onto proj_w [N, D] (times wscale [N]) plus proj_bias:
+    out [B, H, N] in q's dtype."""
+    lib = _lib.load()
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    mask = _mask_arg(mask)
+    proj_w = proj_w.contiguous()
+    B, H, D = q.shape
+    L = k.shape[2]
+    N = proj_w.shape[0]
+    assert tuple(k.shape) == (B, H, L, D) and v.shape == k.shape, \
+        "fused_tree_attn_rmsnorm_linear: k / v must be [B, H, L, D]"
+    assert k.dtype == q.dtype and v.dtype == q.dtype, "fused_tree_attn_rmsnorm_linear: dtypes"
+    assert mask.numel() == L, f"fused_tree_attn_rmsnorm_linear: mask has {mask.numel()} != {L}"
+    assert proj_w.dim() == 2 and proj_w.shape[1] == D, "fused_tree_attn_rmsnorm_linear: proj_w [N, D]"
+    if rms_w is not None:
+        rms_w = rms_w.contiguous().to(torch.float32)
+        assert rms_w.numel() == D
+    if proj_bias is not None:
+        proj_bias = proj_bias.contiguous()
+        assert proj_bias.numel() == N
+    if wscale is not None:
+        wscale = wscale.contiguous().to(torch.float32)
+        assert wscale.numel() == N
+    _on_device("q", q, k=k, v=v, mask=mask, proj_w=proj_w, rms_w=rms_w, proj_bias=proj_bias,
+               wscale=wscale)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty((B, H, N), dtype=q.dtype, device=q.device)
+    wkind = _lib.FP8E4M3 if wscale is not None else code(proj_w.dtype)
+    nbytes = lib.mtp_tree_attn_rmsnorm_linear_workspace_bytes(code(q.dtype), B, H, D, L, wkind, N)
+    ws = _lib.workspace(q.device, nbytes)
+    s = lib.mtp_fused_tree_attn_rmsnorm_linear(
+        ptr(q), code(q.dtype), B, H, D, ptr(k), ptr(v), L, ptr(mask), code(mask.dtype),
+        ptr(proj_w), code(proj_w.dtype), N, ptr(rms_w), _lib.F32 if rms_w is not None else 0,
+        ptr(proj_bias), code(proj_bias.dtype) if proj_bias is not None else 0, ptr(wscale),
+        float(scale), float(eps), ptr(out), ptr(ws), nbytes, _lib.stream_handle(q.device))
+    check(s, "fused_tree_attn_rmsnorm_linear")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# KV step after verify
+def paged_kv_write(k_new: torch.Tensor, v_new: torch.Tensor, k_pages: torch.Tensor,
+                   v_pages: torch.Tensor, page_table: torch.Tensor, start) -> None:
+    """Write the K / V rows of T new tokens into their pages, in place:
+    pages[table[b, p], b, h, p % page_size] = new[b, h, t], p = start + t.
+    k_new / v_new [B, H, T, D] (any strides with d contiguous); pages
+    [P, B, H, page_size, D]; page_table [B, L] int32; start an int, or an
+    int64 device tensor of one element (shared) or [B] (per row)."""
+    lib = _lib.load()
+    assert k_new.dim() == 4 and v_new.shape == k_new.shape, "paged_kv_write: new K / V [B, H, T, D]"
+    if k_new.stride(-1) != 1:
+        k_new = k_new.contiguous()
+    if v_new.stride(-1) != 1 or v_new.stride() != k_new.stride():
+        v_new = v_new.contiguous()
+        k_new = k_new.contiguous()
+    B, H, T, D = k_new.shape
+    assert k_pages.is_contiguous() and v_pages.is_contiguous() and v_pages.shape == k_pages.shape, \
+        "paged_kv_write: pages must be contiguous [P, B, H, page_size, D]"
+    P, _B, _H, ps, _D = k_pages.shape
+    assert (_B, _H, _D) == (B, H, D), "paged_kv_write: pages do not match the new rows"
+    page_table = page_table.contiguous().to(torch.int32)
+    assert page_table.dim() == 2 and page_table.shape[0] == B, "paged_kv_write: page_table [B, L]"
+    start_dev, per_row, start_host = None, 0, 0
+    if torch.is_tensor(start):
+        start_dev = start.contiguous().to(torch.int64)
+        assert start_dev.numel() in (1, B), "paged_kv_write: start must hold 1 or B positions"
+        per_row = int(start_dev.numel() == B and B > 1)
+    else:
+        start_host = int(start)
+    _on_device("k_new", k_new, v_new=v_new, k_pages=k_pages, v_pages=v_pages,
+               page_table=page_table, start=start_dev)
+    sb, sh, st_, _ = k_new.stride()
+    s = lib.mtp_paged_kv_write(ptr(k_new), ptr(v_new), code(k_new.dtype), B, T, H, D, sb, st_, sh,
+                               ptr(k_pages), ptr(v_pages), code(k_pages.dtype), P, ps,
+                               ptr(page_table), page_table.shape[1], ptr(start_dev), per_row,
+                               start_host, _lib.stream_handle(k_new.device))
+    check(s, "paged_kv_write")
+
+
+def verify_commit(accept: torch.Tensor, accepted_n: torch.Tensor, corrected: torch.Tensor,
+                  draft: torch.Tensor, checkpoint: torch.Tensor, kv_len: torch.Tensor,
+                  ids: Optional[torch.Tensor] = None, ids_len: Optional[torch.Tensor] = None):
+    """The engine's verify consumer on the device (no host reads): returns
+    (tokens [B, D + 1] int64, -1 past the width; width int32 [1]) and sets
+    kv_len = checkpoint + width (int64 device scalars; they may be the same
+    tensor); with ids [B, cap] int64 and ids_len (int64 scalar) the tokens
+    are appended at ids_len, which advances by the width."""
+    lib = _lib.load()
+    B, D = draft.shape
+    accept = accept.contiguous().to(torch.int8)
+    accepted_n = accepted_n.contiguous().to(torch.int32)
+    corrected = corrected.contiguous().to(torch.int32)
+    draft = draft.contiguous()
+    if draft.dtype not in (torch.int32, torch.int64):
+        draft = draft.to(torch.int64)
+    for name, t in (("checkpoint", checkpoint), ("kv_len", kv_len)):
+        assert t.dtype == torch.int64 and t.numel() == 1 and t.is_contiguous(), \
+            f"verify_commit: {name} must be a contiguous int64 device scalar"
+    if ids is not None:
+        assert ids.dtype == torch.int64 and ids.dim() == 2 and ids.shape[0] == B and \
+            ids.stride(1) == 1, "verify_commit: ids must be int64 [B, cap] with unit column stride"
+        assert ids_len is not None and ids_len.dtype == torch.int64 and ids_len.numel() == 1
+    _on_device("accepted_n", accepted_n, accept=accept, corrected=corrected, draft=draft,
+               checkpoint=checkpoint, kv_len=kv_len, ids=ids, ids_len=ids_len)
+    dev = accepted_n.device
+    tokens = torch.empty((B, D + 1), dtype=torch.int64, device=dev)
+    width = torch.empty((1,), dtype=torch.int32, device=dev)
+    s = lib.mtp_verify_commit(ptr(accept), ptr(accepted_n), ptr(corrected), ptr(draft),
+                              code(draft.dtype), B, D, ptr(checkpoint), ptr(kv_len), ptr(tokens),
+                              ptr(width), ptr(ids), ids.stride(0) if ids is not None else 0,
+                              ptr(ids_len), _lib.stream_handle(dev))
+    check(s, "verify_commit")
+    return tokens, width
+
+
+def batch_prefix_match(ids: torch.Tensor) -> torch.Tensor:
+    """int32 [R]: per row the length of the prefix it shares with row 0 (L
+    for a full match; zeros when R <= 1)."""
+    lib = _lib.load()
+    ids = ids.contiguous().to(torch.int64)
+    assert ids.dim() == 2, "batch_prefix_match: ids [R, L]"
+    R, L = ids.shape
+    _on_device("ids", ids)
+    out = torch.empty((R,), dtype=torch.int32, device=ids.device)
+    s = lib.mtp_batch_prefix_match(ptr(ids), R, L, ptr(out), _lib.stream_handle(ids.device))
+    check(s, "batch_prefix_match")
+    return out

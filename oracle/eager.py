@@ -392,3 +392,151 @@ def tree_verify_attention(q_nodes, k_pages, v_pages, page_table, page_size: int,
     l = p.sum(dim=-1, keepdim=True)
     out = torch.einsum("hnl,hld->hnd", p / l, vals)
     return out.permute(1, 0, 2).to(q_nodes.dtype)
+
+
+# --------------------------------------------------------------------------- #
+# Draft chain: RMSNorm, add + RMSNorm, greedy token + embedding
+# --------------------------------------------------------------------------- #
+def rmsnorm(x, weight=None, eps: float = 1e-6):
+    """fused_rmsnorm's eager route (mtp_kernels.py:910-933 -> _eager_rmsnorm
+    771-775): the weight is cast to x.dtype by the wrapper (918-920), then
+    (fp32(x) * rsqrt(mean(x^2) + eps) * fp32(weight)) cast to x.dtype."""
+    x = _cpu(x).contiguous()
+    N = x.shape[-1]
+    w = torch.ones(N, dtype=x.dtype) if weight is None else _cpu(weight).to(x.dtype)
+    xf = x.to(torch.float32)
+    ms = (xf * xf).mean(dim=-1, keepdim=True)
+    return (xf * torch.rsqrt(ms + eps) * w.to(torch.float32)).to(x.dtype)
+
+
+def add_rmsnorm(x, residual, weight=None, eps: float = 1e-6):
+    """fused_add_rmsnorm's eager route (mtp_kernels.py:1082-1102 ->
+    _eager_add_rmsnorm 1073-1079): s = fp32(x) + fp32(residual), then the
+    RMSNorm of s with the weight cast to x.dtype, cast to x.dtype."""
+    x, residual = _cpu(x).contiguous(), _cpu(residual).contiguous()
+    N = x.shape[-1]
+    w = torch.ones(N, dtype=x.dtype) if weight is None else _cpu(weight).to(x.dtype)
+    s = x.to(torch.float32) + residual.to(torch.float32)
+    ms = (s * s).mean(dim=-1, keepdim=True)
+    return (s * torch.rsqrt(ms + eps) * w.to(torch.float32)).to(x.dtype)
+
+
+def argmax_tokens(logits, emb_table=None):
+    """argmax_greedy / sample_token(temperature <= 0)
+    (mtp_perf_hardening.py:170-186) = logits.argmax(dim=-1) (int64), and
+    the next step's embedding rows token_embedding(token)
+    (mtp_engine.py:750, 773) when a table is given."""
+    tok = _cpu(logits).argmax(dim=-1)
+    if emb_table is None:
+        return tok
+    return tok, _cpu(emb_table)[tok]
+
+
+# --------------------------------------------------------------------------- #
+# Decode attention (causal, fp8 KV) and the tree monolith
+# --------------------------------------------------------------------------- #
+def causal_attention(q, k, v, scale=None):
+    """fused_causal_attention's eager route (mtp_kernels.py:980-1011 ->
+    _eager_causal_attention 790-801): one query attending every key."""
+    q, k, v = map(_cpu, (q, k, v))
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    return _softmax_attend(q.float(), k.float(), v.float(), scale).to(q.dtype)
+
+
+def causal_attention_fp8(q, k_fp8, v_fp8, kscale, vscale, scale=None):
+    """fused_causal_attention_fp8's eager route (mtp_kernels.py:1105-1133 ->
+    _eager_causal_attention_fp8 817-829): K / V decoded to fp32 and scaled
+    per head (kscale[h], vscale[h]) before the attention."""
+    q, k_fp8, v_fp8, kscale, vscale = map(_cpu, (q, k_fp8, v_fp8, kscale, vscale))
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    kf = k_fp8.to(torch.float32) * kscale.float()[None, :, None, None]
+    vf = v_fp8.to(torch.float32) * vscale.float()[None, :, None, None]
+    return _softmax_attend(q.float(), kf, vf, scale).to(q.dtype)
+
+
+def tree_attn_rmsnorm_linear(q, k, v, mask, proj_w, rms_w=None, proj_bias=None, wscale=None,
+                             scale=None, eps: float = 1e-6):
+    """_eager_tree_attn_rmsnorm_linear (mtp_kernels.py:881-907), the route
+    fused_tree_attn_rmsnorm_linear always takes (1222-1250): masked
+    single-query attention in fp32, RMSNorm over the head dim with rms_w
+    (ones when None), projection onto fp32(proj_w) * wscale[:, None], plus
+    fp32(proj_bias), cast to q.dtype: out [B, H, N]."""
+    q, k, v, mask, proj_w, rms_w, proj_bias, wscale = map(
+        _cpu, (q, k, v, mask, proj_w, rms_w, proj_bias, wscale))
+    B, H, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    valid = (mask > 0.5)[None, None, :].expand(B, H, -1)
+    attn = _softmax_attend(q.float(), k.float(), v.float(), scale, valid)
+    g = torch.ones(D, dtype=torch.float32) if rms_w is None else rms_w.to(torch.float32)
+    ms = (attn * attn).mean(dim=-1, keepdim=True)
+    attn = attn * torch.rsqrt(ms + eps) * g
+    w = proj_w.to(torch.float32)
+    if wscale is not None:
+        w = w * wscale.to(torch.float32)[:, None]
+    out = torch.einsum("bhd,nd->bhn", attn, w)
+    if proj_bias is not None:
+        out = out + proj_bias.to(torch.float32)
+    return out.to(q.dtype)
+
+
+# --------------------------------------------------------------------------- #
+# KV step after verify
+# --------------------------------------------------------------------------- #
+def paged_kv_write(k_new, v_new, k_pages, v_pages, page_table, start):
+    """PagedKVCache.write_inplace (mtp_engine.py:581-585) for every (b, h)
+    and the T new tokens at logical positions start + t: pages[table[b, p],
+    b, h, p % page_size] = new[b, h, t].to(pages.dtype). Returns the updated
+    copies. Positions outside the table or with a page outside [0, P) are
+    skipped (the reference would index page -1, i.e. the last page)."""
+    k_new, v_new, kp, vp, table = map(_cpu, (k_new, v_new, k_pages, v_pages, page_table))
+    kp, vp = kp.clone(), vp.clone()
+    B, H, T, D = k_new.shape
+    P, ps = kp.shape[0], kp.shape[3]
+    st = _cpu(start) if torch.is_tensor(start) else torch.tensor([int(start)])
+    st = st.reshape(-1).to(torch.int64)
+    for b in range(B):
+        s0 = int(st[b] if st.numel() == B and B > 1 else st[0])
+        for t in range(T):
+            p = s0 + t
+            if p < 0 or p >= table.shape[1]:
+                continue
+            pid = int(table[b, p])
+            if pid < 0 or pid >= P:
+                continue
+            kp[pid, b, :, p % ps] = k_new[b, :, t].to(kp.dtype)
+            vp[pid, b, :, p % ps] = v_new[b, :, t].to(vp.dtype)
+    return kp, vp
+
+
+def verify_commit(accept, accepted_n, corrected, draft, checkpoint: int):
+    """generate_fused's verify consumer (mtp_engine.py:1244-1258) with the
+    KVManager bookkeeping it drives (checkpoint, rollback, append,
+    commit_front; 275-331): returns (tokens [B, D + 1] int64 padded with -1,
+    width, new KV length = checkpoint + width)."""
+    a_n, has_reject, new_tokens, kv_advance = engine_rollback(accept, accepted_n, corrected, draft)
+    B, D = _cpu(draft).shape
+    tokens = torch.full((B, D + 1), -1, dtype=torch.int64)
+    w = new_tokens.shape[1]
+    tokens[:, :w] = new_tokens.to(torch.int64)
+    return tokens, w, int(checkpoint) + kv_advance
+
+
+def batch_prefix_match(ids):
+    """RadixKVCache.batch_prefix_match's eager route (mtp_radix.py:195-236):
+    per row the first column differing from row 0, L when none; zeros for
+    R <= 1."""
+    ids = _cpu(ids).to(torch.long)
+    R, L = ids.shape
+    if R <= 1:
+        return torch.zeros((R,), dtype=torch.int32)
+    diff = ids != ids[0:1, :]
+    # a False sentinel column keeps argmax defined for L == 0
+    padded = torch.cat([diff, torch.zeros((R, 1), dtype=torch.bool)], dim=1)
+    first = padded.to(torch.int32).argmax(dim=1)
+    full = torch.full((R,), L, dtype=first.dtype)
+    return torch.where(diff.any(dim=1), first, full).to(torch.int32)

@@ -42,3 +42,16 @@ def close(y, ref, rtol):
     ok = bool((err <= bound).all())
     worst = float((err / (bound + 1e-300)).max()) if ref.numel() else 0.0
     return ok, worst
+
+
+@pytest.fixture
+def tune():
+    """Set library tuning keys (mtp_set_tuning) for one test; every key goes
+    back to the planner's choice afterwards."""
+    from mtp_hip import _lib
+
+    def setter(**keys):
+        _lib.set_tuning(**keys)
+
+    yield setter
+    _lib.set_tuning(**{k: -1 for k in _lib.TUNING_KEYS})

@@ -121,7 +121,7 @@ def test_tree_verify_step_full_size():
 
 
 @pytest.mark.parametrize("chunk_blocks", [1, 3, 5, 20, 36])
-def test_tree_verify_attention_chunkings(chunk_blocks, monkeypatch):
+def test_tree_verify_attention_chunkings(chunk_blocks, tune):
     """Forced chunk lengths (blocks of 64 keys per workgroup) over 35 context
     blocks plus 1 tree block: one block per chunk (36 partials merged), a
     chunk that straddles the context / tree boundary (3), a tree-only chunk
@@ -129,7 +129,7 @@ def test_tree_verify_attention_chunkings(chunk_blocks, monkeypatch):
     window is reloaded mid-chunk)."""
     from mtp_kernels import tree_verify_attention
     from mtp_hip import workloads
-    monkeypatch.setenv("MTP_ATTN_CHUNK_BLOCKS", str(chunk_blocks))
+    tune(attn_chunk_blocks=chunk_blocks)
     g = torch.Generator().manual_seed(chunk_blocks)
     N, H, Lc, D, ps = 64, 3, 2200, 128, 16
     tm = workloads.draft_tree_mask(16, 4)[:N, :N]

@@ -135,15 +135,8 @@ def test_int4_leaves_shared_workspace_counters_zero():
     xl = torch.randn(33, 1024, generator=g).to(torch.bfloat16)
     W = (0.05 * torch.randn(260, 1024, generator=g)).to(torch.bfloat16)
     gm = 1 + 0.1 * torch.randn(1024, generator=g)
-    old = os.environ.get("MTP_SK_SPLITS")
-    os.environ["MTP_SK_SPLITS"] = "3"
-    try:
+    with _lib.tuning(sk_splits=3):
         y = ops.rmsnorm_linear(xl.to(DEV), W.to(DEV), None, 1e-6, 1.0, gamma=gm.to(DEV))
-    finally:
-        if old is None:
-            os.environ.pop("MTP_SK_SPLITS", None)
-        else:
-            os.environ["MTP_SK_SPLITS"] = old
     torch.cuda.synchronize()
     ok, worst = close(y, O.rmsnorm_linear(xl, W, None, 1e-6, 1.0, gamma=gm), 2e-2)
     assert ok, f"worst err/bound = {worst:.3g}"

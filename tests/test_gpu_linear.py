@@ -19,13 +19,22 @@ DEV = "cuda"
 
 @pytest.fixture(autouse=True)
 def _tune_reset():
-    old = {k: os.environ.pop(k, None)
-           for k in ("MTP_WS_TUNE", "MTP_SK_SPLITS", "MTP_SKL", "MTP_SKL_SPLITS", "MTP_SKL_WAVES")}
+    """Every test starts and ends with the planner's own launch choices."""
+    from mtp_hip import _lib
+    _lib.set_tuning(**{k: -1 for k in _lib.TUNING_KEYS})
     yield
-    for k, v in old.items():
-        os.environ.pop(k, None)
-        if v is not None:
-            os.environ[k] = v
+    _lib.set_tuning(**{k: -1 for k in _lib.TUNING_KEYS})
+
+
+def _ws_tune(spec: str) -> None:
+    from mtp_hip import _lib
+    v, sp = (int(t) for t in spec.split(","))
+    _lib.set_tuning(ws_variant=v, ws_splits=sp)
+
+
+def _set(**keys) -> None:
+    from mtp_hip import _lib
+    _lib.set_tuning(**keys)
 
 
 def _inputs(M, N, K, dtype, seed, bias=True, gamma=True):
@@ -64,7 +73,7 @@ def test_rmsnorm_linear_matches_oracle(dtype, M, N, K):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_tile_variants_and_splits(tune, dtype):
     from mtp_hip import ops
-    os.environ["MTP_WS_TUNE"] = tune
+    _ws_tune(tune)
     M, N, K = 40, 1040, 1536
     x, W, b, gm = _inputs(M, N, K, dtype, seed=11)
     print(f"case tune={tune} dtype={dtype}", flush=True)
@@ -133,7 +142,7 @@ def test_fp8_tile_variants_and_splits(tune, M, xdtype):
     16-bit x (four at fp32 x), so some variants stage several x blocks per
     wave and others leave waves without one."""
     from mtp_hip import ops
-    os.environ["MTP_WS_TUNE"] = tune
+    _ws_tune(tune)
     N, K = 592, 1216
     g = torch.Generator().manual_seed(M * 3 + 1)
     W = 0.02 * torch.randn(N, K, generator=g)
@@ -155,7 +164,7 @@ def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
     """The skinny weight-streaming kernel (M <= 64, 16-bit x, fp8 or 16-bit
     W): every forced K-split count, ragged M and N, with and without gamma
     and norm, against the oracle."""
-    os.environ["MTP_SK_SPLITS"] = splits
+    _set(sk_splits=int(splits))
     from mtp_hip import ops
     print(f"case splits={splits} M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
     g = torch.Generator().manual_seed(M * 131 + N + K)
@@ -193,15 +202,15 @@ SKL_CASES = [(None, "8", (40, 40000, 512)), (None, "8", (3, 33024, 256)),
 def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
     """The single-launch skinny kernel (norm applied to the fp32 sums,
     gamma applied while x is staged, 32 * waves columns per workgroup):
-    forced everywhere (MTP_SKL=1) for the small shapes, by default for the
+    forced everywhere (tuning key skl=1) for the small shapes, by default for the
     wide ones (no K-split), with forced and planned K-splits, ragged M and
     N, with and without gamma, bias and norm, against the oracle."""
     M, N, K = shape
     if N <= 32768:
-        os.environ["MTP_SKL"] = "1"
+        _set(skl=1)
     if splits is not None:
-        os.environ["MTP_SKL_SPLITS"] = splits
-    os.environ["MTP_SKL_WAVES"] = waves
+        _set(skl_splits=int(splits))
+    _set(skl_waves=int(waves))
     from mtp_hip import ops
     print(f"case skl splits={splits} waves={waves} M={M} N={N} K={K} w={wkind} x={xdtype}",
           flush=True)

@@ -235,17 +235,128 @@ def test_multi_verify_streaming_path(B, D, K, V):
     _check_chain(out, hidden, W, b, draft, 1e-3)
 
 
-def test_verify_streaming_and_column_group_paths_agree(monkeypatch):
+def test_verify_streaming_and_column_group_paths_agree(tune):
     """The persistent streaming kernel and the column-group kernel
-    (MTP_VERIFY_WSTREAM) give the same tokens wherever the top-2 gap is clear."""
+    (tuning key verify_wstream) give the same tokens wherever the top-2 gap is clear."""
     from mtp_hip import ops
     hidden, W, _, draft, top, gap = _chain_case(6, 4, 1024, 60000, torch.bfloat16, seed=5,
                                                 bias=False)
     hd, Wd, dd = hidden.to(DEV), W.to(DEV), draft.to(DEV)
     a = ops.multi_verify(hd, Wd, dd, None, return_top=True)
-    monkeypatch.setenv("MTP_VERIFY_WSTREAM", "1")
+    tune(verify_wstream=1)
     b = ops.multi_verify(hd, Wd, dd, None, return_top=True)
     torch.cuda.synchronize()
     sure = (gap > 1e-3).reshape(-1)
     assert torch.equal(a[3].cpu().reshape(-1)[sure], b[3].cpu().reshape(-1)[sure])
     assert torch.equal(a[3].cpu().reshape(-1)[sure], top.reshape(-1)[sure].to(torch.int32))
+
+
+# --- any K, any alignment, mixed dtypes: the generic kernel -------------------
+
+GEN_CASES = [
+    # name, hidden dtype, weight dtype, K, bias dtype
+    ("odd_k", torch.bfloat16, torch.bfloat16, 100, None),
+    ("mixed_f32_bf16", torch.float32, torch.bfloat16, 256, None),
+    ("mixed_bf16_f32", torch.bfloat16, torch.float32, 64, torch.float32),
+    ("f16_bias_f32", torch.float16, torch.float16, 96, torch.float32),
+    ("unaligned", torch.bfloat16, torch.bfloat16, 512, None),
+]
+
+
+@pytest.mark.parametrize("name,hdt,wdt,K,bdt", GEN_CASES)
+def test_verify_generic_path(name, hdt, wdt, K, bdt):
+    """Inputs the reference accepts that the streaming kernels do not take:
+    K % 8 != 0, hidden and W of different float dtypes (both upcast as in
+    mtp_fused_verify.py:163), a bias of another dtype, and rows that start
+    2 bytes past a 16-byte boundary (an offset view)."""
+    from mtp_hip import ops
+    M, V = 9, 7000
+    g = torch.Generator().manual_seed(K + V)
+    h = torch.randn(M, K, generator=g).to(hdt)
+    W = (0.05 * torch.randn(V, K, generator=g)).to(wdt)
+    b = None if bdt is None else (0.1 * torch.randn(V, generator=g)).to(bdt)
+    top, gap = O.logits_top(h, W, b)
+    draft = top.clone().to(torch.int64)
+    draft[1::2] = (draft[1::2] + 1) % V
+    hd, Wd = h.to(DEV), W.to(DEV)
+    if name == "unaligned":
+        buf = torch.empty(M * K + 1, dtype=hdt, device=DEV)
+        buf[1:].copy_(hd.reshape(-1))
+        hd = buf[1:].view(M, K)
+        assert hd.data_ptr() % 16 == 2
+        bufw = torch.empty(V * K + 1, dtype=wdt, device=DEV)
+        bufw[1:].copy_(Wd.reshape(-1))
+        Wd = bufw[1:].view(V, K)
+    print(f"case verify-generic {name}", flush=True)
+    acc, t = ops.verify(hd, Wd, draft.to(DEV), None if b is None else b.to(DEV))
+    torch.cuda.synchronize()
+    _check_tokens(t, top, gap, 1e-3)
+    sure = gap > 1e-3
+    assert torch.equal(acc.cpu()[sure], (top == draft.to(torch.int32)).to(torch.int8)[sure])
+    # the chain variant over the same rows
+    B, S = 3, 3
+    hh = h[: B * S].reshape(B, S, K)
+    dd = top[: B * S].reshape(B, S)[:, 1:].clone().to(torch.int64)
+    dd[1, 1] = (dd[1, 1] + 1) % V
+    out = ops.multi_verify(hh.to(DEV), W.to(DEV), dd.to(DEV), None if b is None else b.to(DEV),
+                           return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hh, W, b, dd, 1e-3)
+
+
+@pytest.mark.parametrize("K", [256, 768])
+def test_verify_streaming_path_k_multiple_of_256(K):
+    """The persistent kernel takes K % 256 == 0 (whole rounds of its 4-slot
+    register ring over the 64-k stages of a tile)."""
+    from mtp_hip import ops
+    g = torch.Generator().manual_seed(K)
+    h = torch.randn(12, K, generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(9000, K, generator=g)).to(torch.bfloat16)
+    top, gap = O.logits_top(h, W)
+    _, t = ops.verify(h.to(DEV), W.to(DEV), top.to(DEV))
+    torch.cuda.synchronize()
+    _check_tokens(t, top, gap, 1e-3)
+
+
+def test_persistent_verify_after_other_kernels_with_negative_logits():
+    """The persistent verify kernel after a split-K linear, an INT4 call and
+    a chunked attention on the same stream's workspace (all of which leave
+    scratch data behind the counter prefix), on rows whose logits are all
+    negative (h = -1, W > 0): a stale key would win the atomic max there.
+    Its row keys live in the counter prefix, which every launch leaves at
+    zero."""
+    from mtp_hip import _lib, ops, workloads
+    g = torch.Generator().manual_seed(123)
+    x = torch.randn(48, 1024, generator=g).to(torch.bfloat16)
+    Wl = (0.05 * torch.randn(3000, 1024, generator=g)).to(torch.bfloat16)
+    K, V = 512, 20000
+    h = -torch.ones(6, K).to(torch.bfloat16)
+    Wv = (0.001 + 0.05 * torch.rand(V, K, generator=g)).to(torch.bfloat16)
+    top, gap = O.logits_top(h, Wv)
+    hb = h.reshape(2, 3, K)
+    dr = top.reshape(2, 3)[:, 1:].to(torch.int64)
+    N, H, D, Lc, ps = 64, 4, 128, 1500, 16
+    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    vt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    npg = (Lc + ps - 1) // ps
+    kp = torch.randn(npg, 1, H, ps, D, generator=g).to(torch.bfloat16)
+    vp = torch.randn(npg, 1, H, ps, D, generator=g).to(torch.bfloat16)
+    table = torch.arange(npg).repeat_interleave(ps)[:Lc].reshape(1, Lc).to(torch.int32)
+    tm = workloads.draft_tree_mask(16, 4)[:N, :N]
+    W4 = 0.02 * torch.randn(256, 1024, generator=g)
+    pk, sc = O.quantize_int4(W4, 128, torch.float16, "ref")
+    for rep in range(2):
+        with _lib.tuning(sk_splits=3):
+            ops.rmsnorm_linear(x.to(DEV), Wl.to(DEV), None, 1e-6)
+        ops.int4_matmul(x.to(DEV), pk.to(DEV), sc.to(DEV), 1024, 128, norm=True)
+        from mtp_kernels import tree_verify_attention
+        tree_verify_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), ps, kt.to(DEV),
+                              vt.to(DEV), tm.to(DEV))
+        _, t1 = ops.verify(h.to(DEV), Wv.to(DEV), top.to(DEV))
+        out = ops.multi_verify(hb.to(DEV), Wv.to(DEV), dr.to(DEV), return_top=True)
+        torch.cuda.synchronize()
+        t1 = t1.cpu()
+        assert int(t1.min()) >= 0 and int(t1.max()) < V, rep
+        _check_tokens(t1, top, gap, 1e-4)
+        _check_tokens(out[3], top, gap, 1e-4)
