@@ -29,4 +29,13 @@ AttnKernel attn_merge_pick(int ct, int d) {
 
 void (*attn_generic())(AttnArgs, int, int) { return attn_generic_kernel; }
 
+void (*attn_generic_wide(int d))(AttnArgs, int, int) {
+  if (d <= 512) return attn_generic_wide_kernel<2>;
+  if (d <= 1024) return attn_generic_wide_kernel<4>;
+  if (d <= 2048) return attn_generic_wide_kernel<8>;
+  if (d <= 4096) return attn_generic_wide_kernel<16>;
+  if (d <= kAttnWideMaxD) return attn_generic_wide_kernel<32>;
+  return nullptr;
+}
+
 }  // namespace mtp

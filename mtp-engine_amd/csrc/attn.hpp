@@ -487,4 +487,78 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(const AttnArgs a, int 
   }
 }
 
+// Fallback for head dims above 256 (the tree monolith's single-head shape,
+// D = the hidden size): one 256-thread workgroup per (b, query, head); each
+// thread owns q and the output accumulator at d = t, t + 256, ...; the dot
+// product of every key is reduced over the workgroup (wave shuffles, then a
+// double-buffered LDS slot per wave, one barrier per key).
+template <int NV>
+__global__ void __launch_bounds__(256) attn_generic_wide_kernel(const AttnArgs a, int D, int ct) {
+  __shared__ float red[2][4];
+  const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int qi = blockIdx.y;
+  const int64_t qoff = (int64_t)b * a.q_sb + (int64_t)qi * a.q_sn + (int64_t)h * a.q_sh;
+  float qv[NV], ov[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = th + 256 * i;
+    qv[i] = d < D ? load_as_f32(a.q, ct, qoff + d) : 0.f;
+    ov[i] = 0.f;
+  }
+  const int kdt = a.kv_fp8 ? MTP_FP8E4M3 : ct;
+  const float ks = a.kscale ? a.kscale[h] : 1.f, vs = a.vscale ? a.vscale[h] : 1.f;
+  float m = -INFINITY, l = 0.f;
+  const int total = a.Lc + a.Lt;
+  for (int t = 0; t < total; ++t) {
+    int64_t off;
+    const void *kb, *vb;
+    bool ok = true;
+    if (t < a.Lc) {
+      const int page = a.table[(int64_t)b * a.ld_tab + t];
+      ok = page >= 0 && page < a.npages;
+      off = (int64_t)(ok ? page : 0) * a.p_sp + (int64_t)b * a.p_sb + (int64_t)h * a.p_sh +
+            (int64_t)(t % a.page_size) * D;
+      kb = a.kp;
+      vb = a.vp;
+    } else {
+      const int key = t - a.Lc;
+      off = (int64_t)b * a.d_sb + (int64_t)h * a.d_sh + (int64_t)key * a.d_st;
+      kb = a.kd;
+      vb = a.vd;
+      if (a.mask) ok = mask_on(a.mask, a.mask_dt, a.mask_2d ? (int64_t)qi * a.Lt + key : key);
+    }
+    float sp = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = th + 256 * i;
+      if (d < D) sp += qv[i] * load_kv_f32(kb, kdt, off + d);
+    }
+#pragma unroll
+    for (int w = 32; w > 0; w >>= 1) sp += __shfl_xor(sp, w, 64);
+    if (lane == 0) red[t & 1][wave] = sp;
+    __syncthreads();
+    sp = (red[t & 1][0] + red[t & 1][1]) + (red[t & 1][2] + red[t & 1][3]);
+    const float s = ok ? sp * ks * a.scale : -INFINITY;
+    const float mn = fmaxf(m, s);
+    const bool none = mn == -INFINITY;
+    const float alpha = none ? 1.f : __expf(m - mn);
+    const float p = none ? 0.f : __expf(s - mn);
+    l = l * alpha + p;
+    m = mn;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = th + 256 * i;
+      ov[i] = ov[i] * alpha + (d < D ? p * (load_kv_f32(vb, kdt, off + d) * vs) : 0.f);
+    }
+  }
+  const int64_t ooff = (int64_t)b * a.o_sb + (int64_t)qi * a.o_sn + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = th + 256 * i;
+    if (d < D) store_from_f32(a.out, ct, ooff + d, ov[i] / l);
+  }
+}
+
 }  // namespace mtp

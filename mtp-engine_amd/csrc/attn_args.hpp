@@ -42,5 +42,8 @@ typedef void (*AttnKernel)(AttnArgs);
 AttnKernel attn_pick(int ct, int d);
 AttnKernel attn_merge_pick(int ct, int d);
 void (*attn_generic())(AttnArgs, int, int);
+// Fallback for 256 < D <= kAttnWideMaxD (one workgroup per query), or null.
+constexpr int kAttnWideMaxD = 8192;
+void (*attn_generic_wide(int d))(AttnArgs, int, int);
 
 }  // namespace mtp

@@ -130,7 +130,6 @@ __global__ void __launch_bounds__(256) argmax_rows_kernel(const ArgmaxArgs a) {
   }
   __syncthreads();
   if (!s_last) return;
-  handoff_acquire();
   unsigned long long best = 0ull;
   for (int i = th; i < a.S; i += 256) {
     const unsigned long long p =

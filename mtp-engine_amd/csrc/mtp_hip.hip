@@ -714,8 +714,13 @@ int launch_attention(AttnArgs &a, int ct, int64_t D, void *ws, size_t ws_bytes, 
     }
     return launch_status();
   }
-  if (D > 256) return MTP_ERR_SHAPE;
   dim3 grid((unsigned)(a.B * a.H), (unsigned)a.NQ, 1);
+  if (D > 256) {
+    auto k = attn_generic_wide((int)std::min<int64_t>(D, INT32_MAX));
+    if (!k) return MTP_ERR_SHAPE;
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a, (int)D, ct);
+    return launch_status();
+  }
   hipLaunchKernelGGL(attn_generic(), grid, dim3(64), 0, st, a, (int)D, ct);
   return launch_status();
 }

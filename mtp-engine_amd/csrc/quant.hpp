@@ -67,7 +67,6 @@ fp8_tensor_scale_kernel(const void *x, int dt, int64_t n, float *part, unsigned 
   }
   __syncthreads();
   if (!s_last || threadIdx.x != 0) return;
-  handoff_acquire();
   float am = 0.f;
   for (unsigned b = 0; b < gridDim.x; ++b) am = amax_merge(am, get_f32(part + b));
   scale[0] = am > 0.f ? am / 448.0f : 1.0f;

@@ -424,7 +424,6 @@ sk_kernel(const SkArgs a) {
   if (th == 0) s_flag = (ticket_add(a.ticket + tile) == (unsigned)(a.S - 1));
   __syncthreads();
   if (!s_flag) return;
-  handoff_acquire();
   if (owner) {
     // sums in split order (its own term from registers); the loads of QB
     // splits go out together, one round trip for up to QB splits

@@ -352,7 +352,6 @@ skl_kernel(const SklArgs a) {
   if (th == 0) s_flag = (ticket_add(a.ticket + tile) == (unsigned)(a.S - 1));
   __syncthreads();
   if (!s_flag) return;
-  handoff_acquire();
   // last to arrive: sums in split order (its own terms from registers); the
   // loads of up to QB other splits go out together (one round trip for up
   // to QB + 1 splits)

@@ -232,7 +232,6 @@ skv_kernel(const SkvArgs a) {
   if (th == 0) s_flag = ticket_add(a.ticket) == (unsigned)(grid - 1);
   __syncthreads();
   if (!s_flag) return;
-  handoff_acquire();
   VerifyOut o;
   o.draft = a.draft;
   o.accept = a.accept;

@@ -115,7 +115,6 @@ verify_generic_kernel(const VgenArgs a) {
   if (th == 0) s_flag = ticket_add(a.ticket) == (unsigned)(gridDim.x - 1);
   __syncthreads();
   if (!s_flag) return;
-  handoff_acquire();
   verify_finish(a.keys, M, a.out, s_top, s_draft);
   if (th == 0) ticket_reset(a.ticket);
 }

@@ -473,7 +473,6 @@ wsp_kernel(const WsArgs a) {
   if (th == 0) s_flag = (ticket_add(ticket + grp) == (unsigned)(a.S - 1));
   __syncthreads();
   if (!s_flag) return;
-  handoff_acquire();
   // The last workgroup sums the splits in split order; loads go out four
   // splits at a time (past the last split: zeros) so their latencies
   // overlap, the first four before the row statistics are read.

@@ -517,7 +517,6 @@ wstream_kernel(const WsArgs a) {
     if (th == 0) s_flag = (ticket_add(ticket + grp) == (unsigned)(a.S - 1));
     __syncthreads();
     if (!s_flag) return;
-    handoff_acquire();
     constexpr int Q = NG / 4;
     for (int item = th; item < MPAD * Q; item += NT) {
       const int m = item / Q;
@@ -593,7 +592,6 @@ wstream_kernel(const WsArgs a) {
     if (th == 0) s_flag = (ticket_add(ticket) == (unsigned)(a.G - 1));
     __syncthreads();
     if (!s_flag) return;
-    handoff_acquire();
     // Final argmax over all groups: wave w handles rows w, w + waves, ...
     for (int m = wave; m < Mloc; m += WN * WK) {
       float bv = -__builtin_inff();

@@ -113,3 +113,25 @@ def test_tree_monolith_all_masked_is_nan_and_partial_blocks_are_finite():
     assert bool(torch.isfinite(out.cpu()).all())
     ok, worst = close(out, O.tree_attn_rmsnorm_linear(q, k, v, late, W), 2e-2)
     assert ok, worst
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [512, 1024, 4096])
+def test_wide_head_dim_attention(dtype, D):
+    """Head dims above 256 (the monolith's single-head shape, D = hidden
+    size) run the workgroup-per-query fallback."""
+    import mtp_kernels as mk
+    g = torch.Generator().manual_seed(D)
+    B, H, L = 3, 1, 40
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    k = torch.randn(B, H, L, D, generator=g).to(dtype)
+    v = torch.randn(B, H, L, D, generator=g).to(dtype)
+    mask = (torch.rand(L, generator=g) > 0.5).float()
+    mask[3] = 1.0
+    out = mk.fused_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    out_t = mk.fused_tree_attention(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV))
+    torch.cuda.synchronize()
+    ok, worst = close(out, O.causal_attention(q, k, v), RTOL[dtype])
+    assert ok, f"causal worst err/bound = {worst:.3g}"
+    ok, worst = close(out_t, O.tree_attention(q, k, v, mask), RTOL[dtype])
+    assert ok, f"tree worst err/bound = {worst:.3g}"
