@@ -1,18 +1,22 @@
 """Benchmark of the MI355X verify/draft hot path.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--only a,b] [--no-cpu]
 
 Headline (the `value`): the fused RMSNorm -> linear with fp8-e4m3 weights
 and per-channel fp32 scales, x bf16 [64, 4096] (a 64-node verify tree),
-W [14336, 4096], gamma, bf16 out — algorithmic GB/s of one launch. A step is
-one launch; weights rotate over enough copies that no launch reads W from
-the 256 MB Infinity Cache. Launches go straight through the C ABI with
+W [14336, 4096], gamma, bf16 out — algorithmic GB/s of one call. A step is
+one call; weights rotate over enough copies that no call reads W from the
+256 MB Infinity Cache. Calls go straight through the C ABI with
 preallocated outputs on torch's current stream, timed with HIP events on
-that stream. --all also measures the other workloads (fp32 linear, fp8 at
-M = 8 / 32, multi-verify chain, INT4 linear) into "detail".
+that stream. Every other workload is timed in the same run into "detail"
+(fp8 at M = 8 / 32, the fp32 TF32-off linear, the multi-verify chain, the
+tree-verify step, the INT4 linear at M = 256), each with its roofline
+fraction against its own bound; "verify_step_us" holds the two verify
+steps.
 
-Prints ONE JSON line. The CPU baseline times the oracle's eager restatement
-of the same workload on this host's cores.
+Prints ONE JSON line. The CPU baselines time the oracle's eager
+restatement of the headline workload and of the fp32 configuration on this
+host's cores.
 """
 from __future__ import annotations
 
@@ -32,6 +36,7 @@ for _p in (PKG, ROOT):
 
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
 MALL_BYTES = 256 * 2 ** 20
 
 
@@ -268,6 +273,44 @@ def pmc_traffic(name: str):
         return None
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _time_cpu(fn, seconds):
+    fn()
+    times = []
+    t_end = time.time() + seconds
+    while len(times) < 5 or (time.time() < t_end and len(times) < 20000):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_fp32(torch):
+    """The fp32 RMSNorm+linear configuration (x [16,1024], W [4096,1024],
+    gamma, TF32 off) through the oracle's eager restatement, whole calls."""
+    from mtp_hip import workloads
+    from oracle import eager as O
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    d = workloads.fp32_linear()
+    fn = lambda: O.rmsnorm_linear(d["x"], d["weight"], None, d["eps"], 1.0, gamma=d["gamma"])
+    med, n = _time_cpu(fn, 5.0)
+    M, K = d["x"].shape
+    N = d["weight"].shape[0]
+    nbytes = M * K * 4 + N * K * 4 + K * 4 + M * N * 4
+    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", us_per_call=round(med * 1e6, 1),
+                cores=torch.get_num_threads(), kind="port",
+                sample=f"full fp32 workload, median of {n} calls; {_cpu_model()}")
+
+
 def cpu_baseline_fp8(torch, M: int):
     from mtp_hip import workloads
     from oracle import eager as O
@@ -276,30 +319,15 @@ def cpu_baseline_fp8(torch, M: int):
     d = workloads.fp8_linear(M)
     fn = lambda: O.rmsnorm_linear_fp8(d["x"], d["weight_fp8"], d["wscale"], None, d["eps"],
                                       gamma=d["gamma"])
-    fn()
-    times = []
     # a bounded sample: repeated full calls for about 10 s of CPU work
-    t_end = time.time() + 10.0
-    while len(times) < 5 or (time.time() < t_end and len(times) < 2000):
-        t = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t)
+    med, n = _time_cpu(fn, 10.0)
     N, K = d["weight_fp8"].shape
     nbytes = M * K * 2 + N * K + N * 4 + K * 4 + M * N * 2
-    med = statistics.median(times)
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(),
                 kind="port",
-                sample=f"full workload (M={M}), median of {len(times)} runs, "
+                sample=f"full workload (M={M}), median of {n} runs, "
                        f"{med * 1e3:.1f} ms/run; eager fp32 restatement (fp8 decode + F.linear); "
-                       f"{cpu_model}")
+                       f"{_cpu_model()}")
 
 
 def main():
@@ -307,7 +335,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--all", action="store_true")
+    ap.add_argument("--all", action="store_true", help="(kept for old scripts: every workload "
+                    "is timed by default)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="")
     ap.add_argument("--copy-calib", action="store_true",
@@ -326,14 +355,13 @@ def main():
 
     detail = {}
     headline = None
-    builders = [("fp8_M64", lambda: make_fp8_case(torch, lib, L, 64))]
-    if args.all:
-        builders += [("fp8_M8", lambda: make_fp8_case(torch, lib, L, 8)),
-                     ("fp8_M32", lambda: make_fp8_case(torch, lib, L, 32)),
-                     ("fp32_M16", lambda: make_fp32_case(torch, lib, L)),
-                     ("multi_verify", lambda: make_verify_case(torch, lib, L)),
-                     ("tree_verify", lambda: make_tree_verify_case(torch, lib, L)),
-                     ("int4_M256", lambda: make_int4_case(torch, lib, L))]
+    builders = [("fp8_M64", lambda: make_fp8_case(torch, lib, L, 64)),
+                ("fp8_M8", lambda: make_fp8_case(torch, lib, L, 8)),
+                ("fp8_M32", lambda: make_fp8_case(torch, lib, L, 32)),
+                ("fp32_M16", lambda: make_fp32_case(torch, lib, L)),
+                ("multi_verify", lambda: make_verify_case(torch, lib, L)),
+                ("tree_verify", lambda: make_tree_verify_case(torch, lib, L)),
+                ("int4_M256", lambda: make_int4_case(torch, lib, L))]
     if args.only:
         builders = [b for b in builders if b[0] in args.only.split(",")]
     for key, mk in builders:
@@ -344,9 +372,12 @@ def main():
         us = ms * 1e3
         gbs = case.nbytes / (ms * 1e-3) / 1e9
         tfl = case.flops / (ms * 1e-3) / 1e12
-        detail[key] = dict(workload=case.name, us_per_launch=round(us, 3), GBps=round(gbs, 1),
-                           TFLOPs=round(tfl, 2), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
-                           mfma_frac=round(tfl / BF16_MFMA_PEAK_TFLOPS, 4),
+        hbm_frac = gbs / HBM_PEAK_GBS
+        mfma_frac = tfl / (FP32_MFMA_PEAK_TFLOPS if key == "fp32_M16" else BF16_MFMA_PEAK_TFLOPS)
+        detail[key] = dict(workload=case.name, us_per_call=round(us, 3), GBps=round(gbs, 1),
+                           TFLOPs=round(tfl, 2), bound=case.bound,
+                           roofline_frac=round(hbm_frac if case.bound == "hbm" else mfma_frac, 4),
+                           hbm_frac=round(hbm_frac, 4), mfma_frac=round(mfma_frac, 4),
                            algorithmic_bytes=case.nbytes, flops=case.flops,
                            weight_rotations=case.nrot, steps=steps)
         log(f"[bench] {key}: {us:.2f} us  {gbs:.0f} GB/s  {tfl:.1f} TFLOP/s")
@@ -373,6 +404,10 @@ def main():
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle, fp8 M=64)")
         cpu = cpu_baseline_fp8(torch, 64)
+        log("[bench] cpu baseline (oracle, fp32 configuration)")
+        detail["cpu_baseline_fp32_M16"] = cpu_baseline_fp32(torch)
+    verify_us = {k: detail[k]["us_per_call"] for k in ("multi_verify", "tree_verify")
+                 if k in detail}
 
     case, ms, steps = headline
     gbs = case.nbytes / (ms * 1e-3) / 1e9
@@ -398,6 +433,7 @@ def main():
                      "traffic": pmc_traffic("fp8_rmsnorm_linear_M64.pmc.json"),
                      "algorithmic_bytes": case.nbytes},
         "cpu_baseline": cpu,
+        "verify_step_us": verify_us,
         "detail": detail,
     }
     print(json.dumps(out), flush=True)
