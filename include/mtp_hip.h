@@ -203,6 +203,27 @@ int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B,
                            void *workspace, size_t workspace_bytes,
                            void *stream);
 
+/*
+ * Allocation-free mtp_fused_multi_verify. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as mtp_fused_multi_verify, without the workspace:
+ * the library keeps one static device array of
+ * mtp_noalloc_scratch_bytes() (1 MiB) per GPU, allocated with the module,
+ * and clears its counter prefix with a kernel before each call. Shapes
+ * whose verify workspace (mtp_verify_workspace_bytes) exceeds it return
+ * MTP_ERR_WORKSPACE. Calls on one GPU share the array: calls that overlap
+ * (different streams, no ordering) race.
+ */
+int mtp_fused_multi_verify_noalloc(const void *hidden, int h_dtype, int64_t B,
+                                   int64_t S, int64_t K, const void *weight,
+                                   int w_dtype, int64_t V, const void *bias,
+                                   int bias_dtype, const int32_t *draft,
+                                   int64_t D, int8_t *accept,
+                                   int32_t *accepted_n, int32_t *corrected,
+                                   int32_t *top_out, void *stream);
+size_t mtp_noalloc_scratch_bytes(void);
+
 /* Workspace bytes for mtp_fused_verify (rows = M, seq = 1) or
  * mtp_fused_multi_verify (rows = B * S, seq = S) at vocabulary size V. */
 size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq,

@@ -87,6 +87,10 @@ SIGNATURES = {
         _i, [_vp, _vp, _vp, _vp, _i, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "mtp_batch_prefix_match": (_i, [_vp, _i64, _i64, _vp, _vp]),
     "mtp_workspace_init": (_i, [_vp, _sz, _vp]),
+    "mtp_fused_multi_verify_noalloc": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i64, _vp, _vp, _vp, _vp,
+             _vp]),
+    "mtp_noalloc_scratch_bytes": (_sz, []),
     "mtp_set_tuning": (_i, [ctypes.c_char_p, _i64]),
     "mtp_get_tuning": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
 }
