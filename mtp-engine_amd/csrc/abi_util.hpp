@@ -50,6 +50,9 @@ enum TuneKey {
   kTuneAttnChunkBlocks,  // MTP_ATTN_CHUNK_BLOCKS: key blocks per attention chunk
   kTuneInt4Waves,        // MTP_INT4_WAVES: 4 or 8
   kTuneVerifyWstream,    // MTP_VERIFY_WSTREAM: 1 = column-group verify kernel
+  kTuneSkp,              // MTP_SKP: x-resident skinny kernel, 1 force where it applies, 0 off
+  kTuneSkpSplits,        // MTP_SKP_SPLITS: its K-splits (at least the LDS-bound count)
+  kTuneSkpTa,            // MTP_SKP_TA: its A tiles per wave, 1, 2 or 4
   kTuneCount
 };
 int tune(TuneKey k);

@@ -16,6 +16,7 @@
 #include "quant.hpp"
 #include "sk_args.hpp"
 #include "skl_args.hpp"
+#include "skp_args.hpp"
 #include "skv_args.hpp"
 #include "vgen.hpp"
 #include "ws_dispatch.hpp"
@@ -28,7 +29,7 @@ std::atomic<int> g_tune[kTuneCount];
 std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
-    "attn_chunk_blocks", "int4_waves", "verify_wstream"};
+    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -55,6 +56,9 @@ void tune_init() {
   g_tune[kTuneInt4Waves].store(env_int("MTP_INT4_WAVES", -1), std::memory_order_relaxed);
   if (const char *e = std::getenv("MTP_VERIFY_WSTREAM"))
     if (*e) g_tune[kTuneVerifyWstream].store(1, std::memory_order_relaxed);
+  g_tune[kTuneSkp].store(env_int("MTP_SKP", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkpSplits].store(env_int("MTP_SKP_SPLITS", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkpTa].store(env_int("MTP_SKP_TA", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -540,6 +544,110 @@ int launch_skl(const PlanSkl &p, SklArgs &a, void *ws, hipStream_t st) {
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// x-resident skinny plan (skp.hpp): at most 64 rows of 16-bit x, W of fp8 or
+// the same 16-bit type, whole 128-byte steps per W row. The x rows of a
+// K-split live in LDS (<= kSkpXMaxBytes), so the split count follows from the
+// rows: 1 up to 16 rows (K <= 4096 fp8 / 2048 16-bit W per 16 rows x 128 KB),
+// more above. The column tile (64 TA) is the widest whose grid still covers
+// 7/8 of the CUs. Workspace: counters, split-K partial tiles, sums of squares.
+struct PlanSkp {
+  bool ok = false;
+  int ct = 0, wt = 0, mt = 0, ta = 1;
+  bool gam = false;
+  int G = 0, S = 1, kb_per = 0, nkb = 0;
+  size_t lds = 0, part_off = 0, ss_off = 0, total = 0;
+};
+
+constexpr int kSkpGammaMax = kSkpGammaLoads * kSkpWaves * 256;  // gamma floats per split
+
+// 1 forced, 0 off; by default on, unless a key forces one of the other
+// skinny kernels (sweeps and tests of those)
+int skp_mode() {
+  const int m = tune(kTuneSkp);
+  if (m >= 0) return m;
+  const bool other = tune(kTuneSkl) == 1 || tune(kTuneSkSplits) > 0 ||
+                     tune(kTuneSklSplits) > 0 || tune(kTuneSklWaves) > 0 ||
+                     tune(kTuneWsVariant) >= 0 || tune(kTuneWsSplits) > 0;
+  return other ? 0 : 1;
+}
+
+PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
+  PlanSkp p;
+  p.ct = ct;
+  p.wt = wt;
+  p.gam = gam;
+  if (ct != MTP_BF16 && ct != MTP_F16) return p;
+  if (wt != MTP_FP8E4M3 && wt != ct) return p;
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0) return p;
+  const int wb = dtype_bytes(wt);
+  if ((K * wb) % kSkpStageBytes != 0) return p;
+  const int ks = wt == MTP_FP8E4M3 ? 4 : 2, uk = 32 * ks;
+  // buffer descriptors: x, the workgroup's W rows (32-bit sizes and offsets)
+  if (M * K * 2 >= ((int64_t)1 << 31) || 256 * K * wb >= ((int64_t)1 << 31)) return p;
+  p.mt = (int)((M + 15) / 16);
+  p.nkb = (int)(K * wb / kSkpStageBytes);
+  int smax = kSkpXMaxBytes / (p.mt * ks * 1024);  // steps per split that fit
+  if (gam) smax = std::min(smax, kSkpGammaMax / uk);
+  int S = (p.nkb + smax - 1) / smax;
+  if (tune(kTuneSkpSplits) > 0) S = std::max(S, tune(kTuneSkpSplits));
+  if (S > p.nkb) S = p.nkb;
+  p.kb_per = (p.nkb + S - 1) / S;
+  p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  const int64_t want = (int64_t)device_cus() * 7 / 8;
+  if (tune(kTuneSkpTa) > 0) {
+    const int t = tune(kTuneSkpTa);
+    p.ta = t >= 4 ? 4 : t >= 2 ? 2 : 1;
+  } else {
+    p.ta = 1;
+    for (int t = 4; t >= 2; t /= 2)
+      if ((N + 64 * t - 1) / (64 * t) * p.S >= want) {
+        p.ta = t;
+        break;
+      }
+  }
+  p.G = (int)((N + 64 * p.ta - 1) / (64 * p.ta));
+  if ((int64_t)p.G * p.S > INT32_MAX) return p;
+  if (p.S > 1 && p.G > kCounterSlots) return p;
+  p.lds = skp_lds_bytes(p.mt, ks, p.kb_per, uk, gam);
+  if (p.lds > (size_t)kSkpXMaxBytes + kSkpStaging + (size_t)kSkpGammaMax * 4) return p;
+  size_t off = kCounterBytes;
+  if (p.S > 1) {
+    const size_t part = (size_t)p.S * p.G * kSkpWaves * p.ta * p.mt * 1024;
+    if (part >= ((size_t)1 << 31)) return p;
+    p.part_off = off;
+    off += align_up(part, 256);
+    p.ss_off = off;
+    off += align_up((size_t)p.S * p.G * 64 * sizeof(float), 256);
+  }
+  p.total = off;
+  p.ok = skp_pick(ct, wt, p.mt, p.ta, gam) != nullptr;
+  return p;
+}
+
+int launch_skp(const PlanSkp &p, SkpArgs &a, void *ws, hipStream_t st) {
+  SkpKernel k = skp_pick(p.ct, p.wt, p.mt, p.ta, p.gam);
+  if (!k) return MTP_ERR_DTYPE;
+  unsigned char *w8 = (unsigned char *)ws;
+  a.G = p.G;
+  a.S = p.S;
+  a.kb_per = p.kb_per;
+  a.nkb = p.nkb;
+  if (p.S > 1) {
+    a.part = (float *)(w8 + p.part_off);
+    a.part_ss = (float *)(w8 + p.ss_off);
+    a.ticket = (unsigned *)w8;
+  }
+  const hipError_t e = hipFuncSetAttribute((const void *)k,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
+  if (e != hipSuccess) {
+    note_hip_error(e);
+    return MTP_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(k, dim3((unsigned)(p.G * p.S)), dim3(64 * kSkpWaves), p.lds, st, a);
+  return launch_status();
+}
+
 int launch_generic_linear(const void *x, int xt, const void *w, int wt, const float *wscale,
                           const void *i4scale, int i4dt, int group, int nib, const void *gamma,
                           int gt, const void *bias, int bt, void *y, int64_t M, int64_t N,
@@ -582,6 +690,33 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
+  const int skpm = skp_mode();
+  if (skpm != 0 && aligned && (!gamma || gt == MTP_F32)) {
+    const PlanSkp pp = make_plan_skp(xt, wt, M, N, K, gamma != nullptr);
+    // by default up to 16 rows (one x tile, no K-split at K <= 4096 fp8 /
+    // 2048 16-bit W); above that the split-K hand-off and the per-workgroup
+    // in-place pass cost more than the other kernels' x re-reads (fp8 K 4096
+    // N 14336: 8 rows 15.5 us vs 18.2, 16 rows 17.0 vs 18.5, 32 rows 20.8 vs
+    // 19.9, 64 rows 31 vs 24)
+    if (pp.ok && (tune(kTuneSkp) == 1 || pp.mt == 1)) {
+      if (!ws || ws_bytes < pp.total) return MTP_ERR_WORKSPACE;
+      SkpArgs pa{};
+      pa.x = x;
+      pa.gamma = (const float *)gamma;
+      pa.w = w;
+      pa.wscale = wscale;
+      pa.bias = bias;
+      pa.bias_dt = bt;
+      pa.y = y;
+      pa.M = (int)M;
+      pa.N = (int)N;
+      pa.K = (int)K;
+      pa.norm = norm;
+      pa.eps = eps;
+      pa.scale = scale;
+      return launch_skp(pp, pa, ws, st);
+    }
+  }
   const int sklm = skl_mode();
   if (sklm != 0) {
     const PlanSkl pl = make_plan_skl(xt, wt, M, N, K, gamma != nullptr);
@@ -876,6 +1011,8 @@ size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, in
     if (q.ok && q.total > most) most = q.total;
     PlanSkl l = make_plan_skl(x_dtype, w_kind, M, N, K, gam != 0);
     if (l.ok && l.total > most) most = l.total;
+    PlanSkp q2 = make_plan_skp(x_dtype, w_kind, M, N, K, gam != 0);
+    if (q2.ok && q2.total > most) most = q2.total;
   }
   return most;
 }

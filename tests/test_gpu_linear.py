@@ -242,6 +242,58 @@ def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
     assert torch.equal(y, y3)
 
 
+SKP_CASES = [(None, None, (1, 64, 128)), (None, None, (5, 200, 384)), (None, None, (16, 300, 4096)),
+             ("2", "1", (17, 140, 256)), ("3", "2", (33, 130, 512)), (None, "4", (64, 300, 1024)),
+             (None, None, (48, 1000, 2048)), ("5", None, (64, 2000, 2048)),
+             (None, None, (64, 136, 8192)), (None, "2", (9, 520, 1280)),
+             (None, None, (40, 70, 1344)), (None, None, (40, 70, 1280))]
+
+
+@pytest.mark.parametrize("splits,ta,shape", SKP_CASES)
+@pytest.mark.parametrize("wkind", ["fp8", "same"])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+def test_x_resident_skinny_kernel(splits, ta, shape, wkind, xdtype):
+    """The x-resident skinny kernel (tuning key skp=1): x rows of a K-split
+    copied into LDS once, gamma applied there, norm applied to the fp32
+    sums; planned and forced K-splits and A tiles per wave, ragged M, N and
+    split lengths, with and without gamma, bias and norm, against the
+    oracle, and deterministic bit for bit."""
+    M, N, K = shape
+    if wkind == "same" and K >= 8192:
+        pytest.skip("16-bit W at K 8192 repeats the split counts of fp8 at K 4096")
+    _set(skp=1)
+    if splits is not None:
+        _set(skp_splits=int(splits))
+    if ta is not None:
+        _set(skp_ta=int(ta))
+    from mtp_hip import ops
+    print(f"case skp splits={splits} ta={ta} M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
+    g = torch.Generator().manual_seed(M * 29 + N + K)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(xdtype)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        run = lambda: ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6,
+                                             gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+        y2 = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), None, 1e-6, norm=False)
+        ref2 = O.rmsnorm_linear_fp8(x, wq, ws, None, 1e-6, norm=False)
+    else:
+        Wc = W.to(xdtype)
+        run = lambda: ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5, gamma=gm)
+        y2 = ops.rmsnorm_linear(_dev(x), _dev(Wc), None, 1e-6, 1.0, norm=False)
+        ref2 = O.rmsnorm_linear(x, Wc, None, 1e-6, 1.0, norm=False)
+    y = run()
+    torch.cuda.synchronize()
+    for out, r in ((y, ref), (y2, ref2)):
+        ok, worst = close(out, r, 2e-2)
+        assert ok, f"worst err/bound = {worst:.3g}"
+    assert torch.equal(y, run())
+
+
 @pytest.mark.parametrize("M,N,K,wkind", [(3, 8192, 4096, "same"), (13, 12288, 4096, "fp8")])
 def test_single_launch_default_route_few_rows(M, N, K, wkind):
     """At most 16 rows with at least 48 MiB of W take the single-launch
