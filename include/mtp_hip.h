@@ -147,8 +147,12 @@ int mtp_fused_rmsnorm_linear_fp8(const void *x, int x_dtype, int64_t M,
  * When K % 128 == 0, group % 32 == 0 and packed is 16-byte aligned, the
  * MFMA path runs: it needs the workspace of
  * mtp_rmsnorm_linear_workspace_bytes(x_dtype, MTP_U8, M, N, K) (fp16 copy
- * of xn plus one float per row) and computes with weights decoded to fp16,
- * so |scale| * 8 must stay below 65504 (scales under 2^-14 lose bits).
+ * of xn, one float per row, the scales transposed to fp16 and one float per
+ * column) and computes with weights decoded to fp16. Each column's scales
+ * are first normalised by an exact power of two (undone in the fp32
+ * epilogue), so any finite scale magnitude is safe: a scale is rounded once
+ * to 11 bits, and only scales below 2^-21 of their column's largest lose
+ * more. A non-finite scale makes its column's outputs non-finite.
  * Other shapes run a CUDA-core fallback without workspace.
  */
 int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K,

@@ -1,5 +1,5 @@
 // Grouped INT4 weight-only GEMM for gfx950 (the INT4 RMSNorm -> linear path):
-//   y[m, n] = omul[m] * sum_k xn[m, k] * ((nib(n, k) - 8) * scale[n, k / group])
+//   y[m, n] = omul[m] * cmul[n] * sum_k xn[m, k] * ((nib(n, k) - 8) * scale'[n, k / group])
 //
 // Two launches:
 //  1. int4_prep_kernel. One block per row of x (rows padded to whole tiles):
@@ -16,7 +16,14 @@
 //     order in which the weight decode below produces k.
 //     The remaining blocks transpose the scales, [N, ng] in any float
 //     dtype, to fp16 [ng, ldst], so that the scales of the 32 weight rows a
-//     load instruction serves are 64 contiguous bytes.
+//     load instruction serves are 64 contiguous bytes. Each column n is
+//     first normalised by an exact power of two, 2^-c(n), that brings its
+//     largest |scale| into [2^7, 2^8): the decoded weights (at most 128
+//     times a scale) then stay below 2^15, far from the fp16 limit, and every
+//     scale down to 2^-21 of the column's largest stays a normal fp16 number
+//     (11 bits), whatever the scales' own magnitude (cmul[n] = 2^c(n) undoes
+//     it in the fp32 epilogue). A column whose largest |scale| is inf or NaN
+//     is left as it is (c = 0), so the non-finite value reaches its outputs.
 //  2. int4_gemm_kernel<MT, NA>: 4 waves; wave w owns 32 NA weight rows
 //     (NA 32-row A subtiles) against all 32 MT rows of x of the workgroup
 //     (MT 32-row B tiles); the workgroup covers 128 NA columns of y.
@@ -40,8 +47,9 @@
 //  The row groups of a column group sit on one XCD (workgroups b, b + 8,
 //  b + 16, ... are dispatched to the same XCD), so every read of a weight
 //  tile after the first tends to hit that XCD's L2.
-//  Limits: the decoded weights are fp16, so |scale| * 128 must stay below
-//  65504 and scales below 2^-14 lose precision (fp16 subnormals).
+//  Precision: each scale is rounded once to fp16 (11 bits) after the exact
+//  column normalisation; a scale below 2^-21 of its column's largest loses
+//  bits (fp16 subnormal), a relative contribution already under 2^-21.
 #pragma once
 
 #include <type_traits>
@@ -91,7 +99,7 @@ __device__ __forceinline__ void load8_f32(const void *p, int64_t i, float (&v)[8
 template <int SDT>
 __device__ __forceinline__ void transpose_scales_t(const void *__restrict__ scales, int64_t N,
                                                    int64_t ng, int64_t ldst, int64_t n0,
-                                                   uint16_t *__restrict__ scT) {
+                                                   uint16_t *__restrict__ scT, const float *inv) {
   const int64_t total = 64 * ng;
   for (int64_t i0 = threadIdx.x; i0 < total; i0 += 8 * 256) {
     uint32_t raw[8];
@@ -114,7 +122,7 @@ __device__ __forceinline__ void transpose_scales_t(const void *__restrict__ scal
         if constexpr (SDT == MTP_F32) f = __builtin_bit_cast(float, raw[j]);
         else if constexpr (SDT == MTP_BF16) f = __builtin_bit_cast(float, raw[j] << 16);
         else f = (float)__builtin_bit_cast(_Float16, (uint16_t)raw[j]);
-        scT[g * ldst + n] = __builtin_bit_cast(uint16_t, (_Float16)f);
+        scT[g * ldst + n] = __builtin_bit_cast(uint16_t, (_Float16)(f * inv[n - n0]));
       }
     }
   }
@@ -126,7 +134,7 @@ __device__ __forceinline__ void transpose_scales_t(const void *__restrict__ scal
 template <int SDT>
 __device__ __forceinline__ void transpose_scales_v(const void *__restrict__ scales, int64_t N,
                                                    int64_t ng, int64_t ldst, int64_t n0,
-                                                   uint16_t *__restrict__ scT) {
+                                                   uint16_t *__restrict__ scT, const float *inv) {
   constexpr int EPC = SDT == MTP_F32 ? 4 : 8;  // groups per 16-byte chunk
   const int64_t nch = ng / EPC;
   const int64_t n = n0 + (threadIdx.x & 63);
@@ -162,40 +170,87 @@ __device__ __forceinline__ void transpose_scales_v(const void *__restrict__ scal
                                  : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
         }
       }
+      const float iv = inv[n - n0];
 #pragma unroll
       for (int e = 0; e < EPC; ++e)
-        scT[(c * EPC + e) * ldst + n] = __builtin_bit_cast(uint16_t, (_Float16)f[e]);
+        scT[(c * EPC + e) * ldst + n] = __builtin_bit_cast(uint16_t, (_Float16)(f[e] * iv));
     }
   }
 }
+// |scale| of element i of [N, ng] as the bits of a non-negative float (they
+// order like the values; inf and NaN sort above every finite value).
+__device__ __forceinline__ uint32_t scale_abs_bits(const void *scales, int sdt, int64_t i) {
+  if (sdt == MTP_F32) return ((const uint32_t *)scales)[i] & 0x7fffffffu;
+  const uint32_t h = ((const uint16_t *)scales)[i];
+  const float f = sdt == MTP_BF16 ? __builtin_bit_cast(float, h << 16)
+                                  : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  return __builtin_bit_cast(uint32_t, f) & 0x7fffffffu;
+}
+
+// Columns n0 .. n0 + 63: the normalising powers of two (cmul), then the
+// transpose of the normalised scales to fp16.
 __device__ __forceinline__ void transpose_scales(const void *scales, int sdt, int64_t N,
                                                  int64_t ng, int64_t ldst, int64_t n0,
-                                                 uint16_t *scT) {
+                                                 uint16_t *scT, float *cmul) {
+  __shared__ uint32_t s_mx[64];
+  __shared__ float s_inv[64];
+  const int c = threadIdx.x & 63;
+  const int64_t n = n0 + c;
+  if (threadIdx.x < 64) s_mx[c] = 0u;
+  __syncthreads();
+  if (n < N) {
+    // thread (c, q) takes groups q, q + 4, ...; eight loads go out together
+    uint32_t mx = 0u;
+    for (int64_t g0 = threadIdx.x >> 6; g0 < ng; g0 += 4 * 8) {
+      uint32_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t g = g0 + 4 * j;
+        v[j] = g < ng ? scale_abs_bits(scales, sdt, n * ng + g) : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = max(mx, v[j]);
+    }
+    atomicMax(&s_mx[c], mx);
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const uint32_t mb = s_mx[c];
+    int e = 0;
+    if (mb != 0u && mb < 0x7f800000u) {
+      int ex;
+      frexpf(__builtin_bit_cast(float, mb), &ex);  // 2^(ex-1) <= max < 2^ex
+      e = min(max(ex - 8, -100), 100);             // max * 2^-e in [2^7, 2^8)
+    }
+    s_inv[c] = ldexpf(1.0f, -e);
+    if (n < N) cmul[n] = ldexpf(1.0f, e);
+  }
+  __syncthreads();
   const int epc = sdt == MTP_F32 ? 4 : 8;
   if ((((uintptr_t)scales) & 15) == 0 && ng % epc == 0) {
-    if (sdt == MTP_F32) transpose_scales_v<MTP_F32>(scales, N, ng, ldst, n0, scT);
-    else if (sdt == MTP_BF16) transpose_scales_v<MTP_BF16>(scales, N, ng, ldst, n0, scT);
-    else transpose_scales_v<MTP_F16>(scales, N, ng, ldst, n0, scT);
+    if (sdt == MTP_F32) transpose_scales_v<MTP_F32>(scales, N, ng, ldst, n0, scT, s_inv);
+    else if (sdt == MTP_BF16) transpose_scales_v<MTP_BF16>(scales, N, ng, ldst, n0, scT, s_inv);
+    else transpose_scales_v<MTP_F16>(scales, N, ng, ldst, n0, scT, s_inv);
     return;
   }
-  if (sdt == MTP_F32) transpose_scales_t<MTP_F32>(scales, N, ng, ldst, n0, scT);
-  else if (sdt == MTP_BF16) transpose_scales_t<MTP_BF16>(scales, N, ng, ldst, n0, scT);
-  else transpose_scales_t<MTP_F16>(scales, N, ng, ldst, n0, scT);
+  if (sdt == MTP_F32) transpose_scales_t<MTP_F32>(scales, N, ng, ldst, n0, scT, s_inv);
+  else if (sdt == MTP_BF16) transpose_scales_t<MTP_BF16>(scales, N, ng, ldst, n0, scT, s_inv);
+  else transpose_scales_t<MTP_F16>(scales, N, ng, ldst, n0, scT, s_inv);
 }
 
 // Blocks [0, rows): row m of x -> xn (fp16, fragment-major), omul[m]; rows
-// m >= M are zero. Blocks [rows, rows + ceil(N / 64)): scales -> scT.
+// m >= M are zero. Blocks [rows, rows + ceil(N / 64)): scales -> scT, cmul.
 // XDT: dtype of x; GDT: dtype of gamma, or -1 without gamma.
 template <int XDT, int GDT>
 __global__ void __launch_bounds__(256)
 int4_prep_kernel(const void *x, int64_t M, int64_t K, const void *gamma, float eps, int norm,
                  void *xfv, float *omul, int64_t rows, const void *scales, int sdt, int64_t N,
-                 int64_t ng, int64_t ldst, uint16_t *scT) {
+                 int64_t ng, int64_t ldst, uint16_t *scT, float *cmul) {
   __shared__ float red[2][4];
   u32x4 *xf = (u32x4 *)xfv;
   const int64_t row = blockIdx.x;
   if (row >= rows) {
-    transpose_scales(scales, sdt, N, ng, ldst, (row - rows) * 64, scT);
+    transpose_scales(scales, sdt, N, ng, ldst, (row - rows) * 64, scT, cmul);
     return;
   }
   const int64_t U = K / 128, nq = K / 8;
@@ -313,7 +368,11 @@ int4_gemm_kernel(const I4Args a) {
   static_assert(!KH || NA * MT * 16 * 1024 <= 3 * (MT * 8 * 1024 + BN * 64 + 4 * 1024),
                 "k-half merge fits the LDS stages");
   constexpr int NV = NWL + 1 + ND;        // vector-memory instructions per wave per unit
-  __shared__ __attribute__((aligned(1024))) unsigned char xs[NS * STAGE];
+  // one LDS object (a second one makes the compiler wait for every LDS-DMA
+  // copy before each LDS read of the main loop): the stages, then the
+  // workgroup's column factors cmul
+  __shared__ __attribute__((aligned(1024))) unsigned char xs[NS * STAGE + BN * 4];
+  float *const s_cm = (float *)(xs + NS * STAGE);
 
   const int th = threadIdx.x;
   const int lane = th & 63;
@@ -346,6 +405,14 @@ int4_gemm_kernel(const I4Args a) {
       omr[j] = __builtin_bit_cast(
           float, __builtin_amdgcn_raw_buffer_load_b32(
                      ors, (uint32_t)(rg * MT * 32 + 32 * j + (threadIdx.x & 31)) * 4u, 0, 0));
+  }
+  {
+    // columns past N read 0 (never stored); the main loop's barriers order
+    // these stores before the epilogue's reads
+    const __amdgpu_buffer_rsrc_t crs = make_rsrc(a.cmul, (uint32_t)a.N * 4u);
+    for (int i = th; i < BN; i += 64 * NWV)
+      s_cm[i] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(crs, (uint32_t)(n0 + i) * 4u, 0, 0));
   }
   const int nunits = a.K / UK;
 
@@ -592,7 +659,9 @@ int4_gemm_kernel(const I4Args a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) r4[e] += o[e];
         }
-        const float v0 = r4[0] * om, v1 = r4[1] * om, v2 = r4[2] * om, v3 = r4[3] * om;
+        const float *cm = s_cm + (n - n0);
+        const float v0 = r4[0] * cm[0] * om, v1 = r4[1] * cm[1] * om, v2 = r4[2] * cm[2] * om,
+                    v3 = r4[3] * cm[3] * om;
         if (n + 3 < a.N && a.yvec) {
           uint2 pk;
           if (a.ydt == MTP_BF16) {

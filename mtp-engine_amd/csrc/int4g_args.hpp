@@ -10,7 +10,8 @@ struct I4Args {
   const void *xn;         // fp16 x, fragment-major, rows padded to gm * MT * 32
   const float *omul;      // [M] output multiplier of each row
   const uint8_t *packed;  // [N, K / 2]
-  const void *scales;     // fp16 [ng, ldst], transposed by the prep kernel
+  const void *scales;     // fp16 [ng, ldst], transposed and column-normalised by the prep kernel
+  const float *cmul;      // [ldst] power of two undoing each column's scale normalisation
   int ldst;               // row stride of the transposed scales (>= columns of y covered)
   void *y;                // [M, N] in ydt
   int ydt;
@@ -24,7 +25,7 @@ struct I4Args {
 typedef void (*I4Kernel)(I4Args);
 typedef void (*I4PrepKernel)(const void *, int64_t, int64_t, const void *, float, int, void *,
                              float *, int64_t, const void *, int, int64_t, int64_t, int64_t,
-                             uint16_t *);
+                             uint16_t *, float *);
 // GEMM kernel for MT 32-row x tiles and 128 NA weight rows per workgroup
 // ((1, 1), (2, 1) or (4, 2)) with nw waves (4, or 8: k-halves) for offset-8
 // or (twos) two's-complement nibbles, or null.

@@ -888,11 +888,15 @@ size_t int4_xn_bytes(int64_t M, int64_t K) {
   return align_up((size_t)int4_tiles(M).rows * K * 2, 256);
 }
 size_t int4_omul_bytes(int64_t M) { return align_up((size_t)int4_tiles(M).rows * 4, 256); }
+size_t int4_scT_bytes(int64_t M, int64_t N, int64_t ng) {
+  return align_up((size_t)ng * int4_ldst(M, N) * 2, 256);
+}
 // Workspace: the counter region (left untouched: other entry points keep
-// their arrival tickets there), then xn, omul and the transposed scales.
+// their arrival tickets there), then xn, omul, the transposed scales and the
+// columns' normalising factors.
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t ng) {
-  return kCounterBytes + int4_xn_bytes(M, K) + int4_omul_bytes(M) +
-         align_up((size_t)ng * int4_ldst(M, N) * 2, 256);
+  return kCounterBytes + int4_xn_bytes(M, K) + int4_omul_bytes(M) + int4_scT_bytes(M, N, ng) +
+         align_up((size_t)int4_ldst(M, N) * 4, 256);
 }
 constexpr int64_t kInt4MaxK = (int64_t)1 << 23;  // keeps every buffer offset in 32 bits
 bool int4_fast(int64_t M, int64_t N, int64_t K, int64_t group) {
@@ -925,16 +929,18 @@ int launch_int4(const void *x, int xdt, int64_t M, int64_t K, const uint8_t *pac
   a.xn = w8;
   a.omul = (const float *)(w8 + int4_xn_bytes(M, K));
   uint16_t *scT = (uint16_t *)(w8 + int4_xn_bytes(M, K) + int4_omul_bytes(M));
+  float *cmul = (float *)((unsigned char *)scT + int4_scT_bytes(M, N, ng));
   a.ldst = (int)int4_ldst(M, N);
   I4PrepKernel prep = int4_prep(xdt, gamma ? gdt : -1);
   if (!prep) return MTP_ERR_DTYPE;
   hipLaunchKernelGGL(prep, dim3((unsigned)(tl.rows + sblocks)), dim3(256), 0, st, x, M, K, gamma,
                      eps, norm, (void *)a.xn, (float *)a.omul, tl.rows, scales, sdt, N, ng,
-                     (int64_t)a.ldst, scT);
+                     (int64_t)a.ldst, scT, cmul);
   int s = launch_status();
   if (s != MTP_OK) return s;
   a.packed = packed;
   a.scales = scT;
+  a.cmul = cmul;
   a.y = y;
   a.ydt = xdt;
   a.yvec = xdt != MTP_F32 && N % 4 == 0 && ((uintptr_t)y & 7u) == 0;

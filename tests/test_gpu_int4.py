@@ -56,6 +56,41 @@ def test_int4_rmsnorm_linear_matches_oracle(M, N, K, group, xdtype):
     assert ok, f"worst err/bound = {worst:.3g}"
 
 
+@pytest.mark.parametrize("sdtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("factor", ["tiny", "huge", "mixed"])
+@pytest.mark.parametrize("M,N,K,group", [(33, 300, 512, 128), (256, 260, 1024, 64)])
+def test_int4_extreme_group_scales(M, N, K, group, sdtype, factor):
+    """The MFMA path decodes the weights to fp16 after normalising each
+    column's scales by a power of two: group scales near 1e-6 (fp16
+    subnormal on their own), near 1e3 (decoded weights up to 1.3e5, past the
+    fp16 limit without the normalisation), and columns of both kinds in one
+    matrix, in every scale dtype, against the oracle on the same scales."""
+    print(f"case M={M} N={N} K={K} group={group} s={sdtype} {factor}", flush=True)
+    x, packed, scales, gamma = _case(M, N, K, group, torch.bfloat16, torch.float32, "ref",
+                                     M + N + K)
+    # quantizer scales of 0.02-normal weights are about 1e-2
+    col = torch.arange(N)[:, None]
+    if factor == "tiny":
+        mul = torch.full((N, 1), 1e-4)
+    elif factor == "huge":
+        mul = torch.full((N, 1), 1e5)
+    else:
+        mul = torch.where(col % 2 == 0, torch.tensor(1e-4), torch.tensor(1e5))
+    scales = (scales.float() * mul).to(sdtype)
+    assert torch.isfinite(scales.float()).all()
+    y = _run(x, packed, scales, K, group, "ref", gamma, True)
+    ref = O.int4_matmul(x, packed, scales, K, group, gamma=gamma, norm=True)
+    assert torch.isfinite(y.float()).all()
+    if factor == "mixed":
+        # columns differ by 1e9 in magnitude: each column against its own RMS
+        for sel in (col[:, 0] % 2 == 0, col[:, 0] % 2 == 1):
+            ok, worst = close(y[:, sel], ref[:, sel], RTOL)
+            assert ok, f"worst err/bound = {worst:.3g}"
+    else:
+        ok, worst = close(y, ref, RTOL)
+        assert ok, f"worst err/bound = {worst:.3g}"
+
+
 @pytest.mark.parametrize("nibble", ["ref", "twos"])
 @pytest.mark.parametrize("sdtype", [torch.float16, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K,group", [(8, 256, 512, 128), (70, 136, 256, 32)])
