@@ -53,6 +53,7 @@ enum TuneKey {
   kTuneSkp,              // MTP_SKP: x-resident skinny kernel, 1 force where it applies, 0 off
   kTuneSkpSplits,        // MTP_SKP_SPLITS: its K-splits (at least the LDS-bound count)
   kTuneSkpTa,            // MTP_SKP_TA: its A tiles per wave, 1, 2 or 4
+  kTuneSf32,             // MTP_SF32: small fp32 kernel, 0 off (default on where it applies)
   kTuneCount
 };
 int tune(TuneKey k);

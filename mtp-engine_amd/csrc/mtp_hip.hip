@@ -14,6 +14,7 @@
 #include "generic.hpp"
 #include "int4g_args.hpp"
 #include "quant.hpp"
+#include "sf32_args.hpp"
 #include "sk_args.hpp"
 #include "skl_args.hpp"
 #include "skp_args.hpp"
@@ -29,7 +30,7 @@ std::atomic<int> g_tune[kTuneCount];
 std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
-    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta"};
+    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -59,6 +60,7 @@ void tune_init() {
   g_tune[kTuneSkp].store(env_int("MTP_SKP", -1), std::memory_order_relaxed);
   g_tune[kTuneSkpSplits].store(env_int("MTP_SKP_SPLITS", -1), std::memory_order_relaxed);
   g_tune[kTuneSkpTa].store(env_int("MTP_SKP_TA", -1), std::memory_order_relaxed);
+  g_tune[kTuneSf32].store(env_int("MTP_SF32", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -690,6 +692,26 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
+  // fp32 x and W, <= 16 rows, K <= 1024: one launch, every load in one round
+  // trip (fp32 K 1024 N 4096 16 rows: the planner's tiled kernel 9.9 us)
+  if (xt == MTP_F32 && wt == MTP_F32 && !wscale && tune(kTuneSf32) != 0 && M <= 16 &&
+      K >= 16 && K <= kSf32MaxK && K % 16 == 0 && aligned && (!gamma || gt == MTP_F32) &&
+      tune(kTuneWsVariant) < 0 && tune(kTuneWsSplits) <= 0) {
+    Sf32Args sa{};
+    sa.x = (const float *)x;
+    sa.gamma = (const float *)gamma;
+    sa.w = (const float *)w;
+    sa.bias = bias;
+    sa.bias_dt = bt;
+    sa.y = (float *)y;
+    sa.M = (int)M;
+    sa.N = (int)N;
+    sa.K = (int)K;
+    sa.norm = norm;
+    sa.eps = eps;
+    sa.scale = scale;
+    return launch_sf32(sa, st);
+  }
   const int skpm = skp_mode();
   if (skpm != 0 && aligned && (!gamma || gt == MTP_F32)) {
     const PlanSkp pp = make_plan_skp(xt, wt, M, N, K, gamma != nullptr);

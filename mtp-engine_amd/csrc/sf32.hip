@@ -1,0 +1,19 @@
+// Instantiations and launch of the small fp32 RMSNorm -> linear kernel
+// (sf32.hpp).
+#include "abi_util.hpp"
+#include "sf32.hpp"
+
+namespace mtp {
+
+int launch_sf32(const Sf32Args &a, hipStream_t st) {
+  if (a.M < 1 || a.M > 16 || a.K < 16 || a.K > kSf32MaxK || a.K % 16 != 0 || a.N < 1)
+    return MTP_ERR_SHAPE;
+  const unsigned blocks = (unsigned)((a.N + 15) / 16);
+  if (a.gamma)
+    hipLaunchKernelGGL(sf32_kernel<true>, dim3(blocks), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(sf32_kernel<false>, dim3(blocks), dim3(256), 0, st, a);
+  return launch_status();
+}
+
+}  // namespace mtp

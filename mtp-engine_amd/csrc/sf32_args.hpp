@@ -1,0 +1,27 @@
+// Arguments and launch of the small fp32 RMSNorm -> linear kernel (sf32.hpp),
+// shared by its instantiation unit and the host planner.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace mtp {
+
+struct Sf32Args {
+  const float *x;      // [M, K]
+  const float *gamma;  // [K] or null
+  const float *w;      // [N, K]
+  const void *bias;    // [N] or null
+  int bias_dt;
+  float *y;            // [M, N]
+  int M, N, K;
+  int norm;
+  float eps, scale;
+};
+
+constexpr int kSf32MaxK = 1024;  // k per launch: 4 waves x 16 loads x 16 floats
+
+// Launch for fp32 x and W, 1 <= M <= 16, 16 <= K <= kSf32MaxK with
+// K % 16 == 0, 16-byte aligned x / W / gamma / y (MTP_ERR_SHAPE otherwise).
+int launch_sf32(const Sf32Args &a, hipStream_t st);
+
+}  // namespace mtp

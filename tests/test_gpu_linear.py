@@ -317,6 +317,37 @@ def test_single_launch_default_route_few_rows(M, N, K, wkind):
     assert ok, f"worst err/bound = {worst:.3g}"
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (1, 5, 16), (3, 17, 1008), (16, 130, 512),
+                                   (9, 64, 272), (12, 1000, 48)])
+@pytest.mark.parametrize("bias_dt", [None, torch.float32, torch.bfloat16])
+def test_small_fp32_kernel(M, N, K, bias_dt):
+    """fp32 x and W with at most 16 rows and K <= 1024 take the one-launch
+    fp32 kernel by default (every load of the launch in one round trip):
+    ragged N (scalar stores), K not a multiple of the 256-k wave range,
+    gamma / norm / bias / scale on and off, rtol 1e-5 against the oracle;
+    tuning key sf32=0 gives the tiled kernel the same answer."""
+    from mtp_hip import ops
+    print(f"case sf32 M={M} N={N} K={K} bias={bias_dt}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = None if bias_dt is None else (0.1 * torch.randn(N, generator=g)).to(bias_dt)
+    y = ops.rmsnorm_linear(_dev(x), _dev(W), _dev(b), 1e-6, 0.75, gamma=_dev(gm))
+    ref = O.rmsnorm_linear(x, W, b, 1e-6, 0.75, gamma=gm)
+    y2 = ops.rmsnorm_linear(_dev(x), _dev(W), _dev(b), 1e-6, 1.0, norm=False)
+    ref2 = O.rmsnorm_linear(x, W, b, 1e-6, 1.0, norm=False)
+    torch.cuda.synchronize()
+    for out, r in ((y, ref), (y2, ref2)):
+        ok, worst = close(out, r, 1e-5)
+        assert ok, f"worst err/bound = {worst:.3g}"
+    _set(sf32=0)
+    y3 = ops.rmsnorm_linear(_dev(x), _dev(W), _dev(b), 1e-6, 0.75, gamma=_dev(gm))
+    torch.cuda.synchronize()
+    ok, worst = close(y3, ref, 1e-5)
+    assert ok, f"tiled kernel: worst err/bound = {worst:.3g}"
+
+
 @pytest.mark.parametrize("M", [8, 32, 64])
 def test_fp8_workload_full_size(M):
     """The fp8-e4m3 RMSNorm+linear workload: x bf16 [M,4096], W [14336,4096]."""
