@@ -410,8 +410,9 @@ skp_kernel(const SkpArgs a) {
   __syncthreads();
   if (!s_flag) return;
   // last to arrive: sums in split order (its own terms from registers); the
-  // loads of up to QB other splits go out together
-  constexpr int QB = 4;
+  // loads of QB other splits go out together, at most 32 f32x4 per lane (the
+  // main loop's registers are free by now)
+  constexpr int QB = TA * MT >= 16 ? 2 : TA * MT >= 8 ? 4 : 8;
   f32x4 tot[TA][MT];
 #pragma unroll
   for (int i = 0; i < TA; ++i)
