@@ -54,6 +54,7 @@ enum TuneKey {
   kTuneSkpSplits,        // MTP_SKP_SPLITS: its K-splits (at least the LDS-bound count)
   kTuneSkpTa,            // MTP_SKP_TA: its A tiles per wave, 1, 2 or 4
   kTuneSf32,             // MTP_SF32: small fp32 kernel, 0 off (default on where it applies)
+  kTuneSkpH8,            // MTP_SKP_H8: compact x blocks of the x-resident kernel (<= 8 rows), 0 off
   kTuneCount
 };
 int tune(TuneKey k);

@@ -30,7 +30,7 @@ std::atomic<int> g_tune[kTuneCount];
 std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
-    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32"};
+    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -61,6 +61,7 @@ void tune_init() {
   g_tune[kTuneSkpSplits].store(env_int("MTP_SKP_SPLITS", -1), std::memory_order_relaxed);
   g_tune[kTuneSkpTa].store(env_int("MTP_SKP_TA", -1), std::memory_order_relaxed);
   g_tune[kTuneSf32].store(env_int("MTP_SF32", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkpH8].store(env_int("MTP_SKP_H8", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -556,7 +557,7 @@ int launch_skl(const PlanSkl &p, SklArgs &a, void *ws, hipStream_t st) {
 struct PlanSkp {
   bool ok = false;
   int ct = 0, wt = 0, mt = 0, ta = 1;
-  bool gam = false;
+  bool gam = false, h8 = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
   size_t lds = 0, part_off = 0, ss_off = 0, total = 0;
 };
@@ -589,14 +590,26 @@ PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
   if (M * K * 2 >= ((int64_t)1 << 31) || 256 * K * wb >= ((int64_t)1 << 31)) return p;
   p.mt = (int)((M + 15) / 16);
   p.nkb = (int)(K * wb / kSkpStageBytes);
-  int smax = kSkpXMaxBytes / (p.mt * ks * 1024);  // steps per split that fit
+  // at most 8 rows: compact x blocks (only the parts holding rows 0 .. 7:
+  // half the LDS at fp8, a quarter at 16-bit W, so longer K-splits fit)
+  p.h8 = M <= 8 && tune(kTuneSkpH8) != 0;
+  const int xp = p.h8 ? 8 / (1024 / (2 * uk)) : ks;  // 1 KB parts per x block
+  int smax = kSkpXMaxBytes / (p.mt * xp * 1024);  // steps per split that fit
   if (gam) smax = std::min(smax, kSkpGammaMax / uk);
+  const int64_t want = (int64_t)device_cus() * 7 / 8;
   int S = (p.nkb + smax - 1) / smax;
-  if (tune(kTuneSkpSplits) > 0) S = std::max(S, tune(kTuneSkpSplits));
+  if (tune(kTuneSkpSplits) > 0) {
+    S = std::max(S, tune(kTuneSkpSplits));
+  } else {
+    // enough 64-column workgroups for the CUs, at least 8 steps per split
+    // (beyond a workgroup per CU the split-K hand-off costs more than the x
+    // copies it saves)
+    const int64_t g1 = (N + 63) / 64;
+    while (g1 * S < want && p.nkb / (S + 1) >= 8) ++S;
+  }
   if (S > p.nkb) S = p.nkb;
   p.kb_per = (p.nkb + S - 1) / S;
   p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
-  const int64_t want = (int64_t)device_cus() * 7 / 8;
   if (tune(kTuneSkpTa) > 0) {
     const int t = tune(kTuneSkpTa);
     p.ta = t >= 4 ? 4 : t >= 2 ? 2 : 1;
@@ -611,7 +624,7 @@ PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
   p.G = (int)((N + 64 * p.ta - 1) / (64 * p.ta));
   if ((int64_t)p.G * p.S > INT32_MAX) return p;
   if (p.S > 1 && p.G > kCounterSlots) return p;
-  p.lds = skp_lds_bytes(p.mt, ks, p.kb_per, uk, gam);
+  p.lds = skp_lds_bytes(p.mt, xp, p.kb_per, uk, gam);
   if (p.lds > (size_t)kSkpXMaxBytes + kSkpStaging + (size_t)kSkpGammaMax * 4) return p;
   size_t off = kCounterBytes;
   if (p.S > 1) {
@@ -623,12 +636,12 @@ PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
     off += align_up((size_t)p.S * p.G * 64 * sizeof(float), 256);
   }
   p.total = off;
-  p.ok = skp_pick(ct, wt, p.mt, p.ta, gam) != nullptr;
+  p.ok = skp_pick(ct, wt, p.mt, p.ta, gam, p.h8) != nullptr;
   return p;
 }
 
 int launch_skp(const PlanSkp &p, SkpArgs &a, void *ws, hipStream_t st) {
-  SkpKernel k = skp_pick(p.ct, p.wt, p.mt, p.ta, p.gam);
+  SkpKernel k = skp_pick(p.ct, p.wt, p.mt, p.ta, p.gam, p.h8);
   if (!k) return MTP_ERR_DTYPE;
   unsigned char *w8 = (unsigned char *)ws;
   a.G = p.G;
@@ -715,11 +728,11 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   const int skpm = skp_mode();
   if (skpm != 0 && aligned && (!gamma || gt == MTP_F32)) {
     const PlanSkp pp = make_plan_skp(xt, wt, M, N, K, gamma != nullptr);
-    // by default up to 16 rows (one x tile, no K-split at K <= 4096 fp8 /
-    // 2048 16-bit W); above that the split-K hand-off and the per-workgroup
-    // in-place pass cost more than the other kernels' x re-reads (fp8 K 4096
-    // N 14336: 8 rows 15.5 us vs 18.2, 16 rows 17.0 vs 18.5, 32 rows 20.8 vs
-    // 19.9, 64 rows 31 vs 24)
+    // by default up to 16 rows (one x tile); above that the split-K
+    // hand-off and the per-workgroup in-place pass cost more than the other
+    // kernels' x re-reads (fp8 K 4096 N 14336: 8 rows 14.5 us vs 18.0,
+    // 16 rows 16.4 vs 18.4, 32 rows 20.8 vs 19.9, 64 rows 31 vs 24; 16-bit W
+    // 4096 x 4096, 16 rows: 11.1 vs 14.3)
     if (pp.ok && (tune(kTuneSkp) == 1 || pp.mt == 1)) {
       if (!ws || ws_bytes < pp.total) return MTP_ERR_WORKSPACE;
       SkpArgs pa{};

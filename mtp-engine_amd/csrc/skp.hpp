@@ -58,7 +58,7 @@ __device__ __forceinline__ int skp_xswz(int m) {
   else return (m >> 1) & 7;
 }
 
-template <int CT, int WT, int MT, int TA, bool GAM>
+template <int CT, int WT, int MT, int TA, bool GAM, bool H8>
 __global__ void __launch_bounds__(64 * kSkpWaves, 1)
 skp_kernel(const SkpArgs a) {
   constexpr bool FP8 = WT == MTP_FP8E4M3;
@@ -71,13 +71,19 @@ skp_kernel(const SkpArgs a) {
   constexpr int NS = TA == 1 ? 12 : TA == 2 ? 6 : 4;
   static_assert(NS % 2 == 0, "step parity selects the register set");
   constexpr int BN = 64 * TA;           // columns per workgroup
-  constexpr int NSTMAX = kSkpXMaxBytes / (MT * KS * 1024);  // steps per split at most
   constexpr int RB = 2 * UK;            // x bytes of a row per step
   constexpr int RPI = 1024 / RB;        // rows per 1 KB copy instruction
   constexpr int LPR = RB / 16;          // lanes per row in a copy
+  // parts of 1 KB kept per x block: all KS, or (H8: at most 8 rows, one
+  // 16-row tile) only the ones holding rows 0 .. 7; the B operands of rows
+  // 8 .. 15 then read rows 0 .. 7 again (their outputs are never stored)
+  constexpr int XP = H8 ? 8 / RPI : KS;
+  constexpr int XB = XP * 1024;         // bytes of one x block
+  static_assert(!H8 || MT == 1, "compact blocks hold one tile");
+  constexpr int NSTMAX = kSkpXMaxBytes / (MT * XB);  // steps per split at most
   // x copy instructions of a wave: its steps (all for KS 4, every other one
   // for KS 2) times the tiles
-  constexpr int NCJ = KS == 4 ? NSTMAX : (NSTMAX + 1) / 2;
+  constexpr int NCJ = (NSTMAX + kSkpWaves / XP - 1) / (kSkpWaves / XP);
   static_assert((NS - 1) * NWL + NCJ * MT + kSkpGammaLoads < 64, "vmcnt is 6 bits");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   __shared__ float s_ss[kSkpWaves][64];
@@ -97,8 +103,8 @@ skp_kernel(const SkpArgs a) {
     return q + rot < nst ? q + rot : q + rot - nst;
   };
   unsigned char *const lx = lds;  // x block (step qa, tile t, sub-step s): 1 KB
-  unsigned char *const lw = lds + (size_t)MT * KS * a.kb_per * 1024 + wave * 2048;
-  unsigned char *const lg = lds + (size_t)MT * KS * a.kb_per * 1024 + kSkpStaging;  // gamma
+  unsigned char *const lw = lds + (size_t)MT * XB * a.kb_per + wave * 2048;
+  unsigned char *const lg = lds + (size_t)MT * XB * a.kb_per + kSkpStaging;  // gamma
 
   // epilogue factors of the lane's columns n0 + 16 (w TA + i) + 4 (lane / 16) + e
   float cws[4 * TA], cbi[4 * TA];
@@ -131,8 +137,8 @@ skp_kernel(const SkpArgs a) {
   }
   const uint32_t ldx = (uint32_t)K * 2u;
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)a.M * ldx);
-  const int xh = wave % KS;                       // part of every block this wave copies
-  const int xq0 = KS == 4 ? 0 : wave / 2, xqs = KS == 4 ? 1 : 2;  // its steps: xq0 + xqs j
+  const int xh = wave % XP;                       // part of every block this wave copies
+  const int xq0 = wave / XP, xqs = kSkpWaves / XP;  // its steps: xq0 + xqs j
   const int cm = RPI * xh + lane / LPR;           // copy: row within the tile
   const int cp = lane % LPR;                      // ... its chunk position
   const uint32_t xvo = (uint32_t)cm * ldx + 16u * (uint32_t)(cp ^ skp_xswz<KS>(cm));
@@ -144,7 +150,7 @@ skp_kernel(const SkpArgs a) {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
       if (16 * t + RPI * xh < a.M)
-        sk_lds_copy16<0>(xrs, lx + (qa * MT + t) * (KS * 1024) + xh * 1024,
+        sk_lds_copy16<0>(xrs, lx + (qa * MT + t) * XB + xh * 1024,
                          xvo + (uint32_t)(16 * t) * ldx, (st0 + qa) * RB);
   }
 
@@ -183,22 +189,22 @@ skp_kernel(const SkpArgs a) {
   // overlaps the W stream.
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 1) * NWL) : "memory");
   __syncthreads();
-  float ss[MT][KS];
+  float ss[MT][XP];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int h = 0; h < KS; ++h) ss[t][h] = 0.f;
+    for (int h = 0; h < XP; ++h) ss[t][h] = 0.f;
   // lane's chunk in part h: row RPI h + lane / LPR, position lane % LPR
-  int pc[KS];
+  int pc[XP];
 #pragma unroll
-  for (int h = 0; h < KS; ++h) pc[h] = (lane % LPR) ^ skp_xswz<KS>(RPI * h + lane / LPR);
+  for (int h = 0; h < XP; ++h) pc[h] = (lane % LPR) ^ skp_xswz<KS>(RPI * h + lane / LPR);
   // one step position's blocks, all parts: reads first, then the writes
   auto inplace = [&](int q) __attribute__((always_inline)) {
     const int qa = rotated(q);
-    u32x4 v[MT][KS];
-    f32x4 g[KS][2];
+    u32x4 v[MT][XP];
+    f32x4 g[XP][2];
 #pragma unroll
-    for (int h = 0; h < KS; ++h) {
+    for (int h = 0; h < XP; ++h) {
       if constexpr (GAM) {
         const unsigned char *gp = lg + 4 * (qa * UK + 8 * pc[h]);
         g[h][0] = *(const f32x4 *)gp;
@@ -207,10 +213,10 @@ skp_kernel(const SkpArgs a) {
 #pragma unroll
       for (int t = 0; t < MT; ++t)
         if (16 * t + RPI * h < a.M)
-          v[t][h] = *(const u32x4 *)(lx + (qa * MT + t) * (KS * 1024) + h * 1024 + lane * 16);
+          v[t][h] = *(const u32x4 *)(lx + (qa * MT + t) * XB + h * 1024 + lane * 16);
     }
 #pragma unroll
-    for (int h = 0; h < KS; ++h)
+    for (int h = 0; h < XP; ++h)
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         if (16 * t + RPI * h >= a.M) continue;
@@ -226,7 +232,7 @@ skp_kernel(const SkpArgs a) {
           }
         }
         if constexpr (GAM)
-          *(u32x4 *)(lx + (qa * MT + t) * (KS * 1024) + h * 1024 + lane * 16) = o;
+          *(u32x4 *)(lx + (qa * MT + t) * XB + h * 1024 + lane * 16) = o;
       }
   };
 #pragma unroll
@@ -253,7 +259,10 @@ skp_kernel(const SkpArgs a) {
   // B operand of sub-step s: row ar, chunk KS agp + s of the x block
   uint32_t xrd[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) xrd[s] = ar * RB + 16 * ((KS * agp + s) ^ skp_xswz<KS>(ar));
+  for (int s = 0; s < KS; ++s) {
+    const int xr = H8 ? (ar & 7) : ar;
+    xrd[s] = xr * RB + 16 * ((KS * agp + s) ^ skp_xswz<KS>(xr));
+  }
 
   // Software pipeline, one step deep: step q stages step q + 1's W through
   // LDS and reads back its A operands and x fragments into registers, then
@@ -270,7 +279,7 @@ skp_kernel(const SkpArgs a) {
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        xo[t][s] = *(const u32x4 *)(lx + (qa * MT + t) * (KS * 1024) + xrd[s]);
+        xo[t][s] = *(const u32x4 *)(lx + (qa * MT + t) * XB + xrd[s]);
 #pragma unroll
     for (int i = 0; i < TA; ++i) {
       *(u32x4 *)(lw + st_a0) = wr[slot][2 * i];
@@ -337,12 +346,13 @@ skp_kernel(const SkpArgs a) {
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int h = 0; h < KS; ++h) {
+    for (int h = 0; h < XP; ++h) {
       float r = ss[t][h];
 #pragma unroll
       for (int o = 1; o < LPR; o *= 2) r += __shfl_xor(r, o, 64);
       if (lane % LPR == 0) s_ss[wave][16 * t + RPI * h + lane / LPR] = r;
     }
+  if (H8 && lane < 8) s_ss[wave][8 + lane] = 0.f;  // rows 8 .. 15 (none)
   __syncthreads();
   float ssr = 0.f;  // thread th < 16 MT: row th of this split
   if (th < 16 * MT) ssr = (s_ss[0][th] + s_ss[1][th]) + (s_ss[2][th] + s_ss[3][th]);

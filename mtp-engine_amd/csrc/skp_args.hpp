@@ -37,19 +37,22 @@ typedef void (*SkpKernel)(SkpArgs);
 // Instantiations per x type (skp_bf16.hip, skp_f16.hip): W type fp8 or the
 // same 16-bit type, 16-row x tiles mt 1..4, A tiles per wave ta 1 / 2 / 4,
 // gamma; null for anything else.
-SkpKernel skp_pick_bf16(int wt, int mt, int ta, bool gam);
-SkpKernel skp_pick_f16(int wt, int mt, int ta, bool gam);
-inline SkpKernel skp_pick(int ct, int wt, int mt, int ta, bool gam) {
-  if (ct == MTP_BF16) return skp_pick_bf16(wt, mt, ta, gam);
-  if (ct == MTP_F16) return skp_pick_f16(wt, mt, ta, gam);
+// h8: the compact form for at most 8 rows (mt 1): x blocks keep only the
+// parts holding rows 0 .. 7.
+SkpKernel skp_pick_bf16(int wt, int mt, int ta, bool gam, bool h8);
+SkpKernel skp_pick_f16(int wt, int mt, int ta, bool gam, bool h8);
+inline SkpKernel skp_pick(int ct, int wt, int mt, int ta, bool gam, bool h8) {
+  if (ct == MTP_BF16) return skp_pick_bf16(wt, mt, ta, gam, h8);
+  if (ct == MTP_F16) return skp_pick_f16(wt, mt, ta, gam, h8);
   return nullptr;
 }
 // Dynamic LDS bytes of a launch with `steps` steps (of uk k) per split:
 // x blocks, W staging, gamma of the split's k in whole 1 KB pieces (the
 // copy writes whole pieces).
-inline size_t skp_lds_bytes(int mt, int ks, int steps, int uk, bool gam) {
+// xp: 1 KB parts kept per x block (ks, or 8 rows' worth in the compact form).
+inline size_t skp_lds_bytes(int mt, int xp, int steps, int uk, bool gam) {
   const size_t g = gam ? ((size_t)steps * uk * 4 + 1023) / 1024 * 1024 : 0;
-  return (size_t)mt * ks * steps * 1024 + kSkpStaging + g;
+  return (size_t)mt * xp * steps * 1024 + kSkpStaging + g;
 }
 
 }  // namespace mtp

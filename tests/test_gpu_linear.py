@@ -242,22 +242,29 @@ def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
     assert torch.equal(y, y3)
 
 
-SKP_CASES = [(None, None, (1, 64, 128)), (None, None, (5, 200, 384)), (None, None, (16, 300, 4096)),
-             ("2", "1", (17, 140, 256)), ("3", "2", (33, 130, 512)), (None, "4", (64, 300, 1024)),
-             (None, None, (48, 1000, 2048)), ("5", None, (64, 2000, 2048)),
-             (None, None, (64, 136, 8192)), (None, "2", (9, 520, 1280)),
-             (None, None, (40, 70, 1344)), (None, None, (40, 70, 1280))]
+# (K-splits, A tiles per wave, compact <= 8-row blocks, (M, N, K)); None: planned
+SKP_CASES = [(None, None, None, (1, 64, 128)), (None, None, None, (5, 200, 384)),
+             (None, None, None, (16, 300, 4096)),
+             ("2", "1", None, (17, 140, 256)), ("3", "2", None, (33, 130, 512)),
+             (None, "4", None, (64, 300, 1024)),
+             (None, None, None, (48, 1000, 2048)), ("5", None, None, (64, 2000, 2048)),
+             (None, None, None, (64, 136, 8192)), (None, "2", None, (9, 520, 1280)),
+             (None, None, None, (40, 70, 1344)), (None, None, None, (40, 70, 1280)),
+             (None, None, None, (8, 700, 4096)), ("3", "2", None, (7, 130, 1536)),
+             ("1", "4", None, (2, 300, 1024)), (None, None, None, (8, 1000, 8192)),
+             (None, None, "0", (8, 300, 2048)), ("2", None, "0", (3, 200, 1024))]
 
 
-@pytest.mark.parametrize("splits,ta,shape", SKP_CASES)
+@pytest.mark.parametrize("splits,ta,h8,shape", SKP_CASES)
 @pytest.mark.parametrize("wkind", ["fp8", "same"])
 @pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
-def test_x_resident_skinny_kernel(splits, ta, shape, wkind, xdtype):
+def test_x_resident_skinny_kernel(splits, ta, h8, shape, wkind, xdtype):
     """The x-resident skinny kernel (tuning key skp=1): x rows of a K-split
     copied into LDS once, gamma applied there, norm applied to the fp32
-    sums; planned and forced K-splits and A tiles per wave, ragged M, N and
-    split lengths, with and without gamma, bias and norm, against the
-    oracle, and deterministic bit for bit."""
+    sums; planned and forced K-splits and A tiles per wave, compact and full
+    x blocks for at most 8 rows, ragged M, N and split lengths, with and
+    without gamma, bias and norm, against the oracle, and deterministic bit
+    for bit."""
     M, N, K = shape
     if wkind == "same" and K >= 8192:
         pytest.skip("16-bit W at K 8192 repeats the split counts of fp8 at K 4096")
@@ -266,8 +273,11 @@ def test_x_resident_skinny_kernel(splits, ta, shape, wkind, xdtype):
         _set(skp_splits=int(splits))
     if ta is not None:
         _set(skp_ta=int(ta))
+    if h8 is not None:
+        _set(skp_h8=int(h8))
     from mtp_hip import ops
-    print(f"case skp splits={splits} ta={ta} M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
+    print(f"case skp splits={splits} ta={ta} h8={h8} M={M} N={N} K={K} w={wkind} x={xdtype}",
+          flush=True)
     g = torch.Generator().manual_seed(M * 29 + N + K)
     x = torch.randn(M, K, generator=g).to(xdtype)
     W = 0.05 * torch.randn(N, K, generator=g)
