@@ -1,5 +1,6 @@
 // Instantiations of the attention kernels (attn.hpp).
 #include "attn.hpp"
+#include "attn2.hpp"
 
 namespace mtp {
 
@@ -26,6 +27,14 @@ AttnKernel attn_merge_pick(int ct, int d) {
   }
   return nullptr;
 }
+
+// The 32-query-tile kernel (head dim 128) for a compute type, or null.
+AttnKernel attn2_pick(int ct) {
+  if (ct == MTP_BF16) return attn2_kernel<MTP_BF16>;
+  if (ct == MTP_F16) return attn2_kernel<MTP_F16>;
+  return nullptr;
+}
+int attn2_lds_bytes() { return kAttn2Lds; }
 
 void (*attn_generic())(AttnArgs, int, int) { return attn_generic_kernel; }
 

@@ -140,8 +140,9 @@ attn_kernel(const AttnArgs a) {
   };
   auto fetch = [&](auto slot_c, int j) {
     constexpr int slot = decltype(slot_c)::value;
+    // blocks past the chunk load nothing (their ring slot is never computed)
+    if (j >= nb) return;
     const int gb = cb0 + j;
-    const bool live = j < nb;
     const bool ctx = gb < nctx_all;
     const char *kb_ = ctx ? (const char *)a.kp : (const char *)a.kd;
     const char *vb_ = ctx ? (const char *)a.vp : (const char *)a.vd;
@@ -157,17 +158,19 @@ attn_kernel(const AttnArgs a) {
         bool ok;
         if (ctx) {
           off = s_off[(j % WB) * KB + tk];
-          ok = live && off >= 0;
+          ok = off >= 0;
         } else {
           const int key = (gb - nctx_all) * KB + tk;
-          ok = live && key < a.Lt;
+          ok = key < a.Lt;
           off = (dense_bh + (int64_t)key * a.d_st) * 2;
         }
-        // a missing key reads this head's first query row instead (always valid)
-        const char *kptr = ok ? kb_ + off + dc * 16 : (const char *)qbase + dc * 16;
-        const char *vptr = ok ? vb_ + off + dc * 16 : (const char *)qbase + dc * 16;
-        rk[slot][p][hf] = ld_nt16(kptr);
-        rv[slot][p][hf] = ld_nt16(vptr);
+        // a missing key loads nothing (zeros, masked by its valid bit)
+        rk[slot][p][hf] = u32x4{0u, 0u, 0u, 0u};
+        rv[slot][p][hf] = u32x4{0u, 0u, 0u, 0u};
+        if (ok) {
+          rk[slot][p][hf] = ld_nt16(kb_ + off + dc * 16);
+          rv[slot][p][hf] = ld_nt16(vb_ + off + dc * 16);
+        }
         okm |= (int)ok << (2 * p + hf);
       }
     }
@@ -310,6 +313,7 @@ attn_kernel(const AttnArgs a) {
       static_for<0, R>([&](auto u) {
         constexpr int U = decltype(u)::value;
         const int j = j0 + U;
+        if (j >= nb) return;  // uniform: past the chunk
         put(std::integral_constant<int, (U + 1) % R>{}, std::integral_constant<int, (U + 1) & 1>{});
         const int jn = j + 1 + R;
         if (jn % WB == 0 && jn < nb && cb0 + jn < nctx_all) {
@@ -319,7 +323,7 @@ attn_kernel(const AttnArgs a) {
           __syncthreads();
         }
         fetch(std::integral_constant<int, (U + 1) % R>{}, jn);
-        if (qwave && j < nb) compute(std::integral_constant<int, U & 1>{}, j);
+        if (qwave) compute(std::integral_constant<int, U & 1>{}, j);
         lds_barrier();
       });
     }
@@ -368,12 +372,13 @@ attn_kernel(const AttnArgs a) {
   }
 }
 
-// Chunk merge: workgroup (b*H + h, query tile), thread (query, 4 columns):
-// (M, L, O) <- (M, L, O) (+) (m_c, l_c, O_c) in chunk order, eight chunks of
-// loads in flight; out = O / L (every chunk masked: L = 0 and the output NaN,
-// as the reference's softmax of an all -inf row).
+// Chunk merge: workgroup (b*H + h, kAttnMergeQ queries), thread (query, 4
+// columns): (M, L, O) <- (M, L, O) (+) (m_c, l_c, O_c) in chunk order, eight
+// chunks of loads in flight; out = O / L (every chunk masked: L = 0 and the
+// output NaN, as the reference's softmax of an all -inf row). Small
+// workgroups spread the partial reads over every CU.
 template <int CT, int D>
-__global__ void __launch_bounds__(D * 4)
+__global__ void __launch_bounds__(D / 4 * kAttnMergeQ)
 attn_merge_kernel(const AttnArgs a) {
   constexpr int C4 = D / 4;
   constexpr int F = 8;
@@ -381,7 +386,7 @@ attn_merge_kernel(const AttnArgs a) {
   const int qr = th / C4, d4 = th - (th / C4) * C4;
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int q = blockIdx.y * 16 + qr;
+  const int q = blockIdx.y * kAttnMergeQ + qr;
   if (q >= a.NQ) return;
   const int QP = ((a.NQ + 15) >> 4) * 16;
   const float *pb = a.part + ((int64_t)bh * a.nchunks * QP + q) * D + d4 * 4;

@@ -11,6 +11,7 @@ constexpr int kAttnBlock = 64;         // keys per block (two wave halves of 32)
 constexpr int kAttnRing = 2;           // key blocks in flight per workgroup
 constexpr int kAttnTableWindow = 1024; // context keys whose pages sit in LDS at once
 constexpr float kAttnRescale = 8.f;    // max gain (natural log) before O is rescaled
+constexpr int kAttnMergeQ = 4;         // queries per chunk-merge workgroup
 
 struct AttnArgs {
   const void *q;               // element strides: batch, query, head (d stride 1)
@@ -41,6 +42,10 @@ typedef void (*AttnKernel)(AttnArgs);
 // type, head dim) or null, and the fallback kernel.
 AttnKernel attn_pick(int ct, int d);
 AttnKernel attn_merge_pick(int ct, int d);
+// The 32-query-tile kernel for 33 .. 64 queries at head dim 128 (attn2.hpp)
+// and its dynamic LDS bytes.
+AttnKernel attn2_pick(int ct);
+int attn2_lds_bytes();
 void (*attn_generic())(AttnArgs, int, int);
 // Fallback for 256 < D <= kAttnWideMaxD (one workgroup per query), or null.
 constexpr int kAttnWideMaxD = 8192;

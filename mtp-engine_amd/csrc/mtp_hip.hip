@@ -30,7 +30,7 @@ std::atomic<int> g_tune[kTuneCount];
 std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
-    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8"};
+    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -62,6 +62,7 @@ void tune_init() {
   g_tune[kTuneSkpTa].store(env_int("MTP_SKP_TA", -1), std::memory_order_relaxed);
   g_tune[kTuneSf32].store(env_int("MTP_SF32", -1), std::memory_order_relaxed);
   g_tune[kTuneSkpH8].store(env_int("MTP_SKP_H8", -1), std::memory_order_relaxed);
+  g_tune[kTuneAttn32].store(env_int("MTP_ATTN32", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -851,6 +852,27 @@ AttnPlan make_attn_plan(int ct, int64_t B, int64_t NQ, int64_t H, int64_t D, int
   return p;
 }
 
+// The 32-query-tile kernel takes 33 .. 64 queries at head dim 128 when its
+// buffer descriptors cover the key sources: every valid context row lies in
+// [0, npages * page stride) of the pages and the dense rows of a head span
+// less than 2 GiB (offsets stay below the out-of-range marker).
+bool attn32_usable(const AttnArgs &a, int ct, int64_t D) {
+  if (tune(kTuneAttn32) == 0) return false;
+  if ((ct != MTP_BF16 && ct != MTP_F16) || D != 128 || a.NQ <= 32 || a.NQ > 64) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  if (a.Lc > 0) {
+    if (a.p_sp < 0 || a.p_sb < 0 || a.p_sh < 0 || a.npages <= 0) return false;
+    if ((int64_t)(a.B - 1) * a.p_sb + (int64_t)(a.H - 1) * a.p_sh + (int64_t)a.page_size * D >
+        a.p_sp)
+      return false;
+    if ((int64_t)a.npages * a.p_sp * 2 >= lim) return false;
+  }
+  if (a.Lt > 0) {
+    if (a.d_st < 0 || ((int64_t)(a.Lt - 1) * a.d_st + D) * 2 >= lim) return false;
+  }
+  return true;
+}
+
 // Shared launch path of the three attention entry points. All strides are
 // in elements; the MFMA kernel needs 16-byte aligned rows (strides multiple
 // of 8 elements), the fallback takes anything.
@@ -875,12 +897,25 @@ int launch_attention(AttnArgs &a, int ct, int64_t D, void *ws, size_t ws_bytes, 
       a.ml = (float *)(w8 + p.ml_off);
     }
     dim3 grid((unsigned)(a.B * a.H), (unsigned)p.nchunks, 1);
-    hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a);
+    if (attn32_usable(a, ct, D)) {
+      AttnKernel k2 = attn2_pick(ct);
+      const hipError_t e = hipFuncSetAttribute((const void *)k2,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               attn2_lds_bytes());
+      if (e != hipSuccess) {
+        note_hip_error(e);
+        return MTP_ERR_LAUNCH;
+      }
+      hipLaunchKernelGGL(k2, grid, dim3(512), (size_t)attn2_lds_bytes(), st, a);
+    } else {
+      hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a);
+    }
     if (p.nchunks > 1) {
       int s = launch_status();
       if (s != MTP_OK) return s;
-      hipLaunchKernelGGL(km, dim3((unsigned)(a.B * a.H), (unsigned)p.qt, 1), dim3((unsigned)D * 4),
-                         0, st, a);
+      hipLaunchKernelGGL(km,
+                         dim3((unsigned)(a.B * a.H), (unsigned)((a.NQ + kAttnMergeQ - 1) / kAttnMergeQ), 1),
+                         dim3((unsigned)(D / 4 * kAttnMergeQ)), 0, st, a);
     }
     return launch_status();
   }

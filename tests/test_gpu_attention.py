@@ -164,3 +164,67 @@ def test_tree_verify_attention_head_dims_and_fp16(N, H, Lc, D, dtype):
     ref = O.tree_verify_attention(q, kp, vp, table, ps, kt, vt, tm)
     ok, worst = close(out, ref, 2e-2)
     assert ok, f"worst err/bound = {worst:.3g}"
+
+
+@pytest.mark.parametrize("N,H,Lc,ps", [(33, 2, 130, 16), (48, 3, 1500, 16), (64, 2, 0, 16),
+                                       (64, 2, 100, 5), (57, 1, 4000, 32)])
+def test_tree_verify_attention_query_tilings(N, H, Lc, ps, tune):
+    """33 .. 64 queries at head dim 128 take the 32-query-tile kernel by
+    default; the 16-query-tile kernel (attn32=0) gives the oracle's answer on
+    the same inputs too: context only up to a partial page, odd page sizes,
+    a tree-only key set and a context longer than the page-table window."""
+    from mtp_kernels import tree_verify_attention
+    from mtp_hip import workloads
+    g = torch.Generator().manual_seed(N * 7 + Lc + ps)
+    D = 128
+    tm = workloads.draft_tree_mask(16, 4)[:N, :N]
+    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    vt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kp, vp, table = _paged(g, 1, H, max(Lc, 1), D, ps, torch.bfloat16)
+    table = table[:, :Lc]
+    ref = O.tree_verify_attention(q, kp, vp, table, ps, kt, vt, tm)
+    outs = []
+    for attn32 in (-1, 0):
+        tune(attn32=attn32)
+        print(f"case tree-verify tiling N={N} H={H} Lc={Lc} ps={ps} attn32={attn32}", flush=True)
+        out = tree_verify_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), ps,
+                                    kt.to(DEV), vt.to(DEV), tm.to(DEV)).cpu()
+        ok, worst = close(out, ref, 2e-2)
+        assert ok, f"attn32={attn32}: worst err/bound = {worst:.3g}"
+        outs.append(out)
+    # deterministic: the default kernel repeats itself bit for bit
+    tune(attn32=-1)
+    again = tree_verify_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), ps,
+                                  kt.to(DEV), vt.to(DEV), tm.to(DEV)).cpu()
+    assert torch.equal(again, outs[0])
+
+
+def test_tree_verify_attention_fully_masked_node_is_nan():
+    """A tree node whose mask row is all zero with no context keys: NaN, as
+    the reference's softmax of an all -inf row, on both query tilings."""
+    from mtp_kernels import tree_verify_attention
+    from mtp_hip import _lib, workloads
+    g = torch.Generator().manual_seed(11)
+    N, H, D, ps = 40, 2, 128, 16
+    tm = workloads.draft_tree_mask(16, 4)[:N, :N].clone()
+    tm[5] = 0.0
+    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    vt = torch.randn(N, H, D, generator=g).to(torch.bfloat16)
+    kp, vp, table = _paged(g, 1, H, 1, D, ps, torch.bfloat16)
+    table = table[:, :0]
+    ref = O.tree_verify_attention(q, kp, vp, table, ps, kt, vt, tm)
+    try:
+        for attn32 in (-1, 0):
+            _lib.set_tuning(attn32=attn32)
+            print(f"case tree-verify masked node attn32={attn32}", flush=True)
+            out = tree_verify_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), ps,
+                                        kt.to(DEV), vt.to(DEV), tm.to(DEV)).cpu()
+            assert torch.isnan(out[5].float()).all()
+            keep = torch.ones(N, dtype=torch.bool)
+            keep[5] = False
+            ok, worst = close(out[keep], ref[keep], 2e-2)
+            assert ok, f"attn32={attn32}: worst err/bound = {worst:.3g}"
+    finally:
+        _lib.set_tuning(attn32=-1)
