@@ -187,13 +187,135 @@ __device__ __forceinline__ uint32_t scale_abs_bits(const void *scales, int sdt, 
   return __builtin_bit_cast(uint32_t, f) & 0x7fffffffu;
 }
 
+// Normalising exponent of a column whose largest |scale| has bits mb: c
+// with max * 2^-c in [2^7, 2^8) (0 for an all-zero, inf or NaN column).
+__device__ __forceinline__ int scale_norm_exp(uint32_t mb) {
+  int e = 0;
+  if (mb != 0u && mb < 0x7f800000u) {
+    int ex;
+    frexpf(__builtin_bit_cast(float, mb), &ex);  // 2^(ex-1) <= max < 2^ex
+    e = min(max(ex - 8, -100), 100);
+  }
+  return e;
+}
+
+constexpr int kI4ScaleTileG = 128;  // groups of the one-pass transpose tile
+constexpr int kI4ScaleRow = 68;     // fp16 per LDS tile row (64 columns + pad)
+
+// Columns n0 .. n0 + 63 in one pass (16-byte aligned [N, ng] scales with
+// whole 16-byte chunks per row, ng <= kI4ScaleTileG): every chunk is loaded
+// once, coalesced (consecutive threads take consecutive chunks of a row),
+// into registers; the row maxima meet in LDS; the normalised fp16 values go
+// through an LDS tile [g][n] and leave as 128-byte runs of scT rows.
+// LDS of the scale transposes (one object for every dtype's path)
+struct I4ScaleLds {
+  uint32_t mx[64];
+  float inv[64];
+  __attribute__((aligned(16))) uint16_t t[kI4ScaleTileG * kI4ScaleRow];
+};
+
+template <int SDT>
+__device__ __forceinline__ void transpose_scales_1p(const void *scales, int64_t N, int64_t ng,
+                                                    int64_t ldst, int64_t n0, uint16_t *scT,
+                                                    float *cmul, I4ScaleLds &sl) {
+  constexpr int EPC = SDT == MTP_F32 ? 4 : 8;  // groups per chunk
+  constexpr int CPT = 64 * (kI4ScaleTileG / EPC) / 256;  // chunks per thread at most
+  uint32_t *const s_mx = sl.mx;
+  float *const s_inv = sl.inv;
+  uint16_t *const s_t = sl.t;
+  const int th = threadIdx.x;
+  const int nch = (int)(ng / EPC);
+  const int tot = 64 * nch;
+  if (th < 64) s_mx[th] = 0u;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(N * nch * 16));
+  u32x4 raw[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int i = th + 256 * u;
+    const int r = i / nch, c = i - (i / nch) * nch;
+    raw[u] = bload16(rs, i < tot && n0 + r < N ? (uint32_t)(((n0 + r) * nch + c) * 16) : kOOB);
+  }
+  __syncthreads();  // s_mx cleared
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int i = th + 256 * u;
+    if (i >= tot) break;
+    uint32_t mx = 0u;
+    // the dwords as an array (indexing the vector with the loop counter
+    // read element 0 for every e here)
+    const uint32_t d[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      uint32_t b;
+      if constexpr (SDT == MTP_F32) {
+        b = d[e];
+      } else {
+        const uint32_t h = (e & 1) ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu;
+        b = SDT == MTP_BF16 ? h << 16
+                            : __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h));
+      }
+      mx = max(mx, b & 0x7fffffffu);
+    }
+    atomicMax(&s_mx[i / nch], mx);
+  }
+  __syncthreads();
+  if (th < 64) {
+    const int e = scale_norm_exp(s_mx[th]);
+    s_inv[th] = ldexpf(1.0f, -e);
+    if (n0 + th < N) cmul[n0 + th] = ldexpf(1.0f, e);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int i = th + 256 * u;
+    if (i >= tot) break;
+    const int r = i / nch, c = i - (i / nch) * nch;
+    const float iv = s_inv[r];
+    const uint32_t d[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      float f;
+      if constexpr (SDT == MTP_F32) {
+        f = __builtin_bit_cast(float, d[e]);
+      } else {
+        const uint32_t h = (e & 1) ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu;
+        f = SDT == MTP_BF16 ? __builtin_bit_cast(float, h << 16)
+                            : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+      }
+      s_t[(c * EPC + e) * kI4ScaleRow + r] = __builtin_bit_cast(uint16_t, (_Float16)(f * iv));
+    }
+  }
+  __syncthreads();
+  // row g of the tile -> scT[g][n0 .. n0 + 63]: 8 pieces of 8 columns
+  for (int j = th; j < ng * 8; j += 256) {
+    const int g = j >> 3, p = j & 7;
+    const uint32_t *src = (const uint32_t *)(s_t + g * kI4ScaleRow + 8 * p);
+    const int64_t n = n0 + 8 * p;
+    uint16_t *dst = scT + g * ldst + n;
+    if (n + 7 < N) {
+      *(u32x4 *)dst = u32x4{src[0], src[1], src[2], src[3]};
+    } else {
+      for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = s_t[g * kI4ScaleRow + 8 * p + e];
+    }
+  }
+}
+
 // Columns n0 .. n0 + 63: the normalising powers of two (cmul), then the
 // transpose of the normalised scales to fp16.
 __device__ __forceinline__ void transpose_scales(const void *scales, int sdt, int64_t N,
                                                  int64_t ng, int64_t ldst, int64_t n0,
-                                                 uint16_t *scT, float *cmul) {
-  __shared__ uint32_t s_mx[64];
-  __shared__ float s_inv[64];
+                                                 uint16_t *scT, float *cmul, I4ScaleLds &sl) {
+  {
+    const int epc = sdt == MTP_F32 ? 4 : 8;
+    if ((((uintptr_t)scales) & 15) == 0 && ng % epc == 0 && ng <= kI4ScaleTileG) {
+      if (sdt == MTP_F32) transpose_scales_1p<MTP_F32>(scales, N, ng, ldst, n0, scT, cmul, sl);
+      else if (sdt == MTP_BF16) transpose_scales_1p<MTP_BF16>(scales, N, ng, ldst, n0, scT, cmul, sl);
+      else transpose_scales_1p<MTP_F16>(scales, N, ng, ldst, n0, scT, cmul, sl);
+      return;
+    }
+  }
+  uint32_t *const s_mx = sl.mx;
+  float *const s_inv = sl.inv;
   const int c = threadIdx.x & 63;
   const int64_t n = n0 + c;
   if (threadIdx.x < 64) s_mx[c] = 0u;
@@ -215,13 +337,7 @@ __device__ __forceinline__ void transpose_scales(const void *scales, int sdt, in
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    const uint32_t mb = s_mx[c];
-    int e = 0;
-    if (mb != 0u && mb < 0x7f800000u) {
-      int ex;
-      frexpf(__builtin_bit_cast(float, mb), &ex);  // 2^(ex-1) <= max < 2^ex
-      e = min(max(ex - 8, -100), 100);             // max * 2^-e in [2^7, 2^8)
-    }
+    const int e = scale_norm_exp(s_mx[c]);
     s_inv[c] = ldexpf(1.0f, -e);
     if (n < N) cmul[n] = ldexpf(1.0f, e);
   }
@@ -238,41 +354,11 @@ __device__ __forceinline__ void transpose_scales(const void *scales, int sdt, in
   else transpose_scales_t<MTP_F16>(scales, N, ng, ldst, n0, scT, s_inv);
 }
 
-// Blocks [0, rows): row m of x -> xn (fp16, fragment-major), omul[m]; rows
-// m >= M are zero. Blocks [rows, rows + ceil(N / 64)): scales -> scT, cmul.
-// XDT: dtype of x; GDT: dtype of gamma, or -1 without gamma.
-template <int XDT, int GDT>
-__global__ void __launch_bounds__(256)
-int4_prep_kernel(const void *x, int64_t M, int64_t K, const void *gamma, float eps, int norm,
-                 void *xfv, float *omul, int64_t rows, const void *scales, int sdt, int64_t N,
-                 int64_t ng, int64_t ldst, uint16_t *scT, float *cmul) {
-  __shared__ float red[2][4];
-  u32x4 *xf = (u32x4 *)xfv;
-  const int64_t row = blockIdx.x;
-  if (row >= rows) {
-    transpose_scales(scales, sdt, N, ng, ldst, (row - rows) * 64, scT, cmul);
-    return;
-  }
-  const int64_t U = K / 128, nq = K / 8;
-  if (row >= M) {
-    for (int64_t q = threadIdx.x; q < nq; q += 256)
-      xf[xfrag_piece(row, q, U)] = u32x4{0u, 0u, 0u, 0u};
-    if (threadIdx.x == 0) omul[row] = 0.f;
-    return;
-  }
-  const int64_t base = row * K;
-  float ss = 0.f, mx = 0.f;  // sum of x^2, max |x * gamma|
-#pragma unroll 4
-  for (int64_t q = threadIdx.x; q < nq; q += 256) {
-    float v[8], g[8];
-    load8_f32<XDT>(x, base + 8 * q, v);
-    if constexpr (GDT >= 0) load8_f32<GDT>(gamma, 8 * q, g);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ss += v[i] * v[i];
-      mx = fmaxf(mx, fabsf(GDT >= 0 ? v[i] * g[i] : v[i]));
-    }
-  }
+// Row statistics of the prep: the workgroup's sums (sum of x^2, max
+// |x * gamma|) reduced, rstd r (norm) or 1, the power of two 2^e that brings
+// max |x * r * gamma| into [2^14, 2^15] (omul[row] = 2^e); returns r 2^-e.
+__device__ __forceinline__ float int4_row_stats(float ss, float mx, float (&red)[2][4], int64_t K,
+                                                float eps, int norm, float *omul, int64_t row) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     ss += __shfl_xor(ss, o, 64);
@@ -293,26 +379,101 @@ int4_prep_kernel(const void *x, int64_t M, int64_t K, const void *gamma, float e
     frexpf(top, &ex);  // top <= 2^ex < 2 top
     e = min(max(ex - 15, -100), 100);
   }
-  const float mul = ldexpf(r, -e);
   if (threadIdx.x == 0) omul[row] = ldexpf(1.0f, e);
+  return ldexpf(r, -e);
+}
+
+// 16-byte xn piece of 8 consecutive k (first even): x * mul * gamma, odd k
+// times 1/16, rounded to fp16, in the decode's slot order.
+template <int GDT>
+__device__ __forceinline__ u32x4 int4_xpiece(const float (&v)[8], const float (&g)[8], float mul) {
+  _Float16 hv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float t = v[i] * ((i & 1) ? mul * 0.0625f : mul);
+    if constexpr (GDT >= 0) t *= g[i];
+    hv[slot8(i)] = (_Float16)t;
+  }
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = (uint32_t)__builtin_bit_cast(uint16_t, hv[2 * j]) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, hv[2 * j + 1]) << 16);
+  return o;
+}
+
+// Blocks [0, rows): row m of x -> xn (fp16, fragment-major), omul[m]; rows
+// m >= M are zero. Blocks [rows, rows + ceil(N / 64)): scales -> scT, cmul.
+// XDT: dtype of x; GDT: dtype of gamma, or -1 without gamma.
+template <int XDT, int GDT>
+__global__ void __launch_bounds__(256)
+int4_prep_kernel(const void *x, int64_t M, int64_t K, const void *gamma, float eps, int norm,
+                 void *xfv, float *omul, int64_t rows, const void *scales, int sdt, int64_t N,
+                 int64_t ng, int64_t ldst, uint16_t *scT, float *cmul) {
+  __shared__ float red[2][4];
+  __shared__ I4ScaleLds sl;
+  u32x4 *xf = (u32x4 *)xfv;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) {
+    transpose_scales(scales, sdt, N, ng, ldst, (row - rows) * 64, scT, cmul, sl);
+    return;
+  }
+  const int64_t U = K / 128, nq = K / 8;
+  if (row >= M) {
+    for (int64_t q = threadIdx.x; q < nq; q += 256)
+      xf[xfrag_piece(row, q, U)] = u32x4{0u, 0u, 0u, 0u};
+    if (threadIdx.x == 0) omul[row] = 0.f;
+    return;
+  }
+  const int64_t base = row * K;
+  float ss = 0.f, mx = 0.f;  // sum of x^2, max |x * gamma|
+  if (nq <= 4 * 256) {
+    // K <= 8192: the row (and gamma) stay in registers, one round trip
+    float v[4][8], g[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t q = threadIdx.x + 256 * u;
+      if (q < nq) {
+        load8_f32<XDT>(x, base + 8 * q, v[u]);
+        if constexpr (GDT >= 0) load8_f32<GDT>(gamma, 8 * q, g[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (threadIdx.x + 256 * u >= nq) break;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ss += v[u][i] * v[u][i];
+        mx = fmaxf(mx, fabsf(GDT >= 0 ? v[u][i] * g[u][i] : v[u][i]));
+      }
+    }
+    const float mul = int4_row_stats(ss, mx, red, K, eps, norm, omul, row);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t q = threadIdx.x + 256 * u;
+      if (q >= nq) break;
+      xf[xfrag_piece(row, q, U)] = int4_xpiece<GDT>(v[u], g[u], mul);
+    }
+    return;
+  }
 #pragma unroll 4
   for (int64_t q = threadIdx.x; q < nq; q += 256) {
     float v[8], g[8];
     load8_f32<XDT>(x, base + 8 * q, v);
     if constexpr (GDT >= 0) load8_f32<GDT>(gamma, 8 * q, g);
-    _Float16 hv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float t = v[i] * ((i & 1) ? mul * 0.0625f : mul);
-      if constexpr (GDT >= 0) t *= g[i];
-      hv[slot8(i)] = (_Float16)t;
+      ss += v[i] * v[i];
+      mx = fmaxf(mx, fabsf(GDT >= 0 ? v[i] * g[i] : v[i]));
     }
-    u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o[j] = (uint32_t)__builtin_bit_cast(uint16_t, hv[2 * j]) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, hv[2 * j + 1]) << 16);
-    xf[xfrag_piece(row, q, U)] = o;
+  }
+  const float mul = int4_row_stats(ss, mx, red, K, eps, norm, omul, row);
+#pragma unroll 4
+  for (int64_t q = threadIdx.x; q < nq; q += 256) {
+    float v[8], g[8];
+    load8_f32<XDT>(x, base + 8 * q, v);
+    if constexpr (GDT >= 0) load8_f32<GDT>(gamma, 8 * q, g);
+    xf[xfrag_piece(row, q, U)] = int4_xpiece<GDT>(v, g, mul);
   }
 }
 
