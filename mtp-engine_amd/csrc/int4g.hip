@@ -4,21 +4,21 @@
 namespace mtp {
 
 template <bool TWOS>
-static I4Kernel int4_gemm_pick_t(int mt, int na, int nw) {
-  if (nw == 4) {
-    if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1, 4, TWOS>;
-    if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1, 4, TWOS>;
-    if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2, 4, TWOS>;
-  } else if (nw == 8) {
-    if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1, 8, TWOS>;
-    if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1, 8, TWOS>;
-    if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2, 8, TWOS>;
+static I4Kernel int4_gemm_pick_t(int mt, int na, int layout) {
+  if (layout == kI4Rows4) {
+    if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1, 4, false, TWOS>;
+    if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1, 4, false, TWOS>;
+    if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2, 4, false, TWOS>;
+  } else if (layout == kI4Rows4KHalves) {
+    if (mt == 1 && na == 1) return int4_gemm_kernel<1, 1, 8, true, TWOS>;
+    if (mt == 2 && na == 1) return int4_gemm_kernel<2, 1, 8, true, TWOS>;
+    if (mt == 4 && na == 2) return int4_gemm_kernel<4, 2, 8, true, TWOS>;
   }
   return nullptr;
 }
 
-I4Kernel int4_gemm_pick(int mt, int na, int nw, bool twos) {
-  return twos ? int4_gemm_pick_t<true>(mt, na, nw) : int4_gemm_pick_t<false>(mt, na, nw);
+I4Kernel int4_gemm_pick(int mt, int na, int layout, bool twos) {
+  return twos ? int4_gemm_pick_t<true>(mt, na, layout) : int4_gemm_pick_t<false>(mt, na, layout);
 }
 
 template <int XDT>

@@ -508,14 +508,16 @@ __device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
   return d;
 }
 
-template <int MT, int NA, int NWV, bool TWOS>
+template <int MT, int NA, int NWV, bool KH, bool TWOS>
 __global__ void __launch_bounds__(64 * NWV, 1)
 int4_gemm_kernel(const I4Args a) {
-  // NWV = 8: waves split each unit's k-steps in halves (wave = row quarter
-  // + 4 k-half), two waves per SIMD; the halves' sums meet in LDS at the end
-  constexpr bool KH = NWV == 8;
+  // KH: waves split each unit's k-steps in halves (wave = row group + RQ
+  // k-half); the halves' sums meet in LDS at the end. RQ row groups of NA
+  // 32-row A subtiles each: 8 waves x NA 2 (two waves per SIMD), or 4 waves
+  // x NA 4 (one wave per SIMD, 256 accumulators: half the x reads per MFMA)
+  constexpr int RQ = KH ? NWV / 2 : NWV;  // row groups
   constexpr int KSW = KH ? 4 : 8;         // k-steps per wave per unit
-  constexpr int BN = 128 * NA, UK = 128;
+  constexpr int BN = 32 * NA * RQ, UK = 128;
   constexpr int TILE = 8 * 1024;          // bytes of one 32-row x tile per unit
   constexpr int XST = MT * TILE;          // x bytes of one LDS stage
   constexpr int WST = BN * 64;            // weight bytes of one LDS stage (64 per row)
@@ -526,8 +528,11 @@ int4_gemm_kernel(const I4Args a) {
   constexpr int NWL = BN / 16 / NWV;      // weight copies per wave per unit (16 rows each)
   static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
   static_assert((8 * MT) % NWV == 0 && (BN / 16) % NWV == 0, "copies divide among the waves");
-  static_assert(!KH || NA * MT * 16 * 1024 <= 3 * (MT * 8 * 1024 + BN * 64 + 4 * 1024),
+  static_assert(!KH || RQ * NA * MT * 4 * 1024 <= 3 * (MT * 8 * 1024 + BN * 64 + 4 * 1024),
                 "k-half merge fits the LDS stages");
+  // scale copy of a unit: KH with 8 waves, two waves per run (half the rows
+  // each); otherwise one wave per run
+  constexpr int SPARTS = KH ? NWV / 4 : 1;
   constexpr int NV = NWL + 1 + ND;        // vector-memory instructions per wave per unit
   // one LDS object (a second one makes the compiler wait for every LDS-DMA
   // copy before each LDS read of the main loop): the stages, then the
@@ -541,8 +546,8 @@ int4_gemm_kernel(const I4Args a) {
   // offset (which depends on it) in scalar registers, without a waterfall
   const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
   const int h = lane >> 5, l32 = lane & 31;
-  const int rq = KH ? wave & 3 : wave;  // row quarter: A tiles NA rq .. NA rq + NA - 1
-  const int kh = KH ? wave >> 2 : 0;    // k-half (k-steps 4 kh .. 4 kh + 3)
+  const int rq = KH ? wave % RQ : wave;  // row group: A tiles NA rq .. NA rq + NA - 1
+  const int kh = KH ? wave / RQ : 0;     // k-half (k-steps 4 kh .. 4 kh + 3)
 
   // blockIdx -> (column group, row group): the row groups of column group
   // c are workgroups with b % 8 == c % 8 (one XCD).
@@ -607,14 +612,14 @@ int4_gemm_kernel(const I4Args a) {
   // land on the other half).
   const __amdgpu_buffer_rsrc_t srs =
       make_rsrc((const uint16_t *)a.scales + n0, (uint32_t)(a.ng * a.ldst - n0) * 2u);
-  const int srun = KH ? wave & 3 : wave;
+  const int srun = wave & 3;
   // a group of a multiple of 128 k covers the whole unit: its four runs
   // share one scale per row, so only run 0 is copied and read (the other
   // copies go to the zero-byte descriptor, keeping the per-unit count of
   // vector-memory instructions of every wave)
   const bool one_run = a.group % 128 == 0;
   const bool scopy = !one_run || srun == 0;
-  const uint32_t shalf = KH ? (uint32_t)(wave >> 2) * BN : 0u;  // bytes
+  const uint32_t shalf = (uint32_t)(wave >> 2) * (BN / SPARTS) * 2u;  // bytes
   const uint32_t svo = lane < BN / 8 ? (uint32_t)lane * 16u + shalf : kOOB;
   const uint32_t ldst2 = (uint32_t)a.ldst * 2u;
   // x tiles of this workgroup: MT consecutive 32-row tiles of the
@@ -647,8 +652,8 @@ int4_gemm_kernel(const I4Args a) {
       const int k = su * UK + 32 * srun;
       const int g = a.glog >= 0 ? k >> a.glog : k / a.group;
       unsigned char *dst = xs + slot * STAGE + XST + WST + srun * 1024 + shalf;
-      if constexpr (KH) {
-        if (lane < BN / 16)
+      if constexpr (SPARTS > 1) {
+        if (lane < BN / 8 / SPARTS)
           lds_copy16(live && scopy ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));
       } else {
         lds_copy16(live && scopy ? srs : nrs, dst, svo, (int)((uint32_t)g * ldst2));

@@ -937,21 +937,30 @@ bool mask_dt_ok(int dt) { return is_float_dt(dt) || dt == MTP_U8; }
 // then the decode-in-register GEMM. Workspace: the fp16 copy (rows padded
 // to whole row groups) at 0, omul after it.
 struct Int4Tiles {
-  int mt, na;   // 32-row x tiles and 128-row weight groups per workgroup
-  int64_t gm;   // row groups
-  int64_t rows; // padded rows
+  int mt, na;    // 32-row x tiles, 32-row weight subtiles per wave row group
+  int layout;    // wave layout (kI4Rows4, kI4Rows4KHalves, kI4Rows2KHalves)
+  int bn;        // weight rows per workgroup
+  int64_t gm;    // row groups
+  int64_t rows;  // padded rows
 };
+// Tiles and wave layout for M rows. Up to 64 rows: 4 waves on 4 row groups.
+// Beyond: 8 waves (4 row groups x 2 k-halves, two waves per SIMD) by
+// default (M 256, K 8192, N 28672: 127 us against 132 with 4 waves); the
+// int4_waves tuning key (4 or 8) overrides.
 Int4Tiles int4_tiles(int64_t M) {
   Int4Tiles t;
   t.mt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
+  t.layout = t.mt == 4 ? kI4Rows4KHalves : kI4Rows4;
+  if (tune(kTuneInt4Waves) > 0) t.layout = tune(kTuneInt4Waves) == 8 ? kI4Rows4KHalves : kI4Rows4;
   t.na = t.mt == 4 ? 2 : 1;
+  t.bn = int4_bn(t.na);
   t.gm = (M + 32 * t.mt - 1) / (32 * t.mt);
   t.rows = t.gm * 32 * t.mt;
   return t;
 }
 // Row stride of the transposed fp16 scales: the columns the GEMM covers.
 int64_t int4_ldst(int64_t M, int64_t N) {
-  const int64_t bn = 128 * int4_tiles(M).na;
+  const int64_t bn = int4_tiles(M).bn;
   return (N + bn - 1) / bn * bn;
 }
 size_t int4_xn_bytes(int64_t M, int64_t K) {
@@ -983,14 +992,10 @@ int launch_int4(const void *x, int xdt, int64_t M, int64_t K, const uint8_t *pac
   if (!ws || ws_bytes < int4_ws_bytes(M, N, K, ng)) return MTP_ERR_WORKSPACE;
   if (((uintptr_t)ws & 15u) != 0) return MTP_ERR_ALIGN;
   const Int4Tiles tl = int4_tiles(M);
-  // 8 waves (k-halves, two waves per SIMD) on the largest tile: M 256,
-  // K 8192, N 28672 137 us against 143 us with 4; MTP_INT4_WAVES=4|8
-  // overrides (tuning)
-  int nw = tl.mt == 4 ? 8 : 4;
-  if (tune(kTuneInt4Waves) > 0) nw = tune(kTuneInt4Waves) == 8 ? 8 : 4;
-  I4Kernel gemm = int4_gemm_pick(tl.mt, tl.na, nw, nibble == MTP_NIBBLE_TWOS);
+  const int nw = tl.layout == kI4Rows4KHalves ? 8 : 4;
+  I4Kernel gemm = int4_gemm_pick(tl.mt, tl.na, tl.layout, nibble == MTP_NIBBLE_TWOS);
   if (!gemm) return MTP_ERR_DTYPE;
-  const int64_t gn = (N + 128 * tl.na - 1) / (128 * tl.na);
+  const int64_t gn = (N + tl.bn - 1) / tl.bn;
   const int64_t blocks = (gn + 7) / 8 * 8 * tl.gm;
   const int64_t sblocks = (N + 63) / 64;  // scale-transpose blocks of the prep launch
   if (blocks > INT32_MAX || tl.rows + sblocks > INT32_MAX) return MTP_ERR_SHAPE;
