@@ -10,9 +10,9 @@ int launch_sf32(const Sf32Args &a, hipStream_t st) {
     return MTP_ERR_SHAPE;
   const unsigned blocks = (unsigned)((a.N + 15) / 16);
   if (a.gamma)
-    hipLaunchKernelGGL(sf32_kernel<true>, dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((sf32_kernel<true, kSf32Waves>), dim3(blocks), dim3(64 * kSf32Waves), 0, st, a);
   else
-    hipLaunchKernelGGL(sf32_kernel<false>, dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((sf32_kernel<false, kSf32Waves>), dim3(blocks), dim3(64 * kSf32Waves), 0, st, a);
   return launch_status();
 }
 

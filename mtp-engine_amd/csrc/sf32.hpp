@@ -8,14 +8,15 @@
 // W [4096, 1024]) moves 16.8 MB and is bound by launch latency and the
 // first round trip, not by sustained bandwidth. So every workgroup takes
 // only 16 columns (N / 16 workgroups: 256 for N = 4096, every CU), and
-// every load of the launch goes out at once: wave w of the 4 covers
-// k = 256 w .. 256 w + 255; lane l = 16 g + r holds, for each of 16 loads
-// i, W[n0 + r] and x[r] (and gamma) at k = 256 w + 16 i + 4 g .. + 3, which
-// is exactly its slot of 4 consecutive v_mfma_f32_16x16x4_f32 (A = W rows,
-// B = x rows, k-slot g): no LDS staging. Each load instruction reads 64
-// contiguous bytes of 16 rows. x * gamma is formed in fp32 registers and
-// the squares of x are summed on the way; the 4 waves' 16x16 sums and row
-// squares meet in LDS in a fixed order.
+// every load of the launch goes out at once: wave w of the NW covers
+// k = KPW w .. KPW w + KPW - 1 (KPW = 1024 / NW); lane l = 16 g + r holds,
+// for each of its loads i, W[n0 + r] and x[r] (and gamma) at k = KPW w +
+// 16 i + 4 g .. + 3, which is exactly its slot of 4 consecutive
+// v_mfma_f32_16x16x4_f32 (A = W rows, B = x rows, k-slot g): no LDS
+// staging. Each load instruction reads 64 contiguous bytes of 16 rows.
+// x * gamma is formed in fp32 registers and the squares of x are summed on
+// the way; the waves' 16x16 sums and row squares meet in LDS in a fixed
+// order.
 #pragma once
 
 #include "mtp_common.hpp"
@@ -24,11 +25,13 @@
 
 namespace mtp {
 
-template <bool GAM>
-__global__ void __launch_bounds__(256, 1) sf32_kernel(const Sf32Args a) {
-  __shared__ f32x4 s_acc[4][64];
-  __shared__ float s_ss[4][16];
-  __shared__ f32x4 s_g[4][64];
+template <bool GAM, int NW>
+__global__ void __launch_bounds__(64 * NW, 1) sf32_kernel(const Sf32Args a) {
+  constexpr int KPW = kSf32MaxK / NW;  // k per wave
+  constexpr int CPW = KPW / 16;        // 16-k chunks (4 MFMA k-slots x 4) per wave
+  __shared__ f32x4 s_acc[NW][64];
+  __shared__ float s_ss[NW][16];
+  __shared__ f32x4 s_g[NW][64];
   const int th = threadIdx.x, lane = th & 63;
   const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
   const int g = lane >> 4, r = lane & 15;
@@ -39,33 +42,33 @@ __global__ void __launch_bounds__(256, 1) sf32_kernel(const Sf32Args a) {
       make_rsrc(a.w + (int64_t)n0 * K, (uint32_t)(min(16, a.N - n0) * K) * 4u);
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)(a.M * K) * 4u);
   const __amdgpu_buffer_rsrc_t grs = make_rsrc(a.gamma, GAM ? (uint32_t)K * 4u : 0u);
-  // float offset of load i: row r, k = 256 w + 16 i + 4 g; chunks at or past K
-  // (K % 16 == 0) use an out-of-range offset
-  f32x4 wv[16], xv[16], gv[16];
+  // Load order: gamma first (every MFMA needs it), then W and x of chunk i
+  // side by side, so the MFMAs of chunk i start as soon as its two loads are
+  // back instead of after the whole round trip.
+  // gamma of the wave's KPW k: one load (lane L < KPW / 4: k KPW w + 4 L ..
+  // + 3), then each lane reads its CPW chunks back from LDS (lanes of one
+  // group read the same address)
+  f32x4 gl = f32x4{1.f, 1.f, 1.f, 1.f};
+  if constexpr (GAM)
+    gl = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                   grs, lane < KPW / 4 ? (uint32_t)(KPW * wave + 4 * lane) * 4u : kOOB, 0, 0));
+  // float offset of load i: row r, k = KPW w + 16 i + 4 g; chunks at or past
+  // K (K % 16 == 0) use an out-of-range offset
+  f32x4 wv[CPW], xv[CPW], gv[CPW];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int k = 256 * wave + 16 * i + 4 * g;
-    const bool live = 256 * wave + 16 * i < K;
+  for (int i = 0; i < CPW; ++i) {
+    const int k = KPW * wave + 16 * i + 4 * g;
+    const bool live = KPW * wave + 16 * i < K;
     const uint32_t ro = live ? (uint32_t)(r * K + k) * 4u : kOOB;
     wv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, ro, 0, 2));
+    xv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ro, 0, 0));
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int k = 256 * wave + 16 * i + 4 * g;
-    const bool live = 256 * wave + 16 * i < K;
-    xv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          xrs, live ? (uint32_t)(r * K + k) * 4u : kOOB, 0, 0));
-  }
-  // gamma of the wave's 256 k: one load (lane L: k 256 w + 4 L .. + 3), then
-  // each lane reads its 16 chunks back from LDS (lanes of one group read the
-  // same address)
   if constexpr (GAM) {
-    const f32x4 gl = __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(grs, (uint32_t)(256 * wave + 4 * lane) * 4u, 0, 0));
     s_g[wave][lane] = gl;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) gv[i] = s_g[wave][4 * i + g];
+    for (int i = 0; i < CPW; ++i) gv[i] = s_g[wave][4 * i + g];
   }
   // epilogue factors of the lane's outputs: columns n0 + 4 g + e
   float cws[4], cbi[4];
@@ -78,7 +81,7 @@ __global__ void __launch_bounds__(256, 1) sf32_kernel(const Sf32Args a) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) ac[e] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < CPW; ++i) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float xe = xv[i][e];
@@ -95,9 +98,14 @@ __global__ void __launch_bounds__(256, 1) sf32_kernel(const Sf32Args a) {
   s_acc[wave][lane] = acc;
   __syncthreads();
   if (wave != 0) return;
-  // lane holds D[n = 4 g + e][m = r]
-  const f32x4 t = ((s_acc[0][lane] + s_acc[1][lane]) + s_acc[2][lane]) + s_acc[3][lane];
-  const float sq = ((s_ss[0][r] + s_ss[1][r]) + s_ss[2][r]) + s_ss[3][r];
+  // lane holds D[n = 4 g + e][m = r]; the waves' sums in wave order
+  f32x4 t = s_acc[0][lane];
+  float sq = s_ss[0][r];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    t += s_acc[w][lane];
+    sq += s_ss[w][r];
+  }
   const float rs = a.norm ? 1.0f / sqrtf(sq / (float)K + a.eps) : 1.0f;
   const int m = r;
   if (m >= a.M) return;
