@@ -104,6 +104,22 @@ def test_int4_reference_mode_scales_and_nibbles(M, N, K, group, sdtype, nibble):
     assert ok, f"worst err/bound = {worst:.3g}"
 
 
+@pytest.mark.parametrize("sdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,group", [(40, 200, 8192, 64), (40, 130, 4352, 32),
+                                         (70, 90, 1024, 32)])
+def test_int4_scale_transpose_paths(M, N, K, group, sdtype):
+    """The prep's scale transpose at the edges of its one-pass form: 128
+    groups per row (the largest it takes), 136 groups (the two-pass form),
+    ragged N (a last block of 26 columns) with 32 groups per row; x rows of
+    8192 and 4352 (registers / loop)."""
+    print(f"case int4 scales M={M} N={N} K={K} group={group} s={sdtype}", flush=True)
+    x, packed, scales, gamma = _case(M, N, K, group, torch.bfloat16, sdtype, "ref", M * N + K)
+    y = _run(x, packed, scales, K, group, "ref", gamma, True)
+    ref = O.int4_matmul(x, packed, scales, K, group, gamma=gamma, norm=True)
+    ok, worst = close(y, ref, RTOL)
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
 def test_int4_no_norm_row_ranges():
     """norm=False rows of very different magnitude (1e-6 .. 1e4, a zero row):
     each row is brought to fp16 with its own power of two."""
