@@ -30,7 +30,7 @@ std::atomic<int> g_tune[kTuneCount];
 std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
-    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32"};
+    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -63,6 +63,7 @@ void tune_init() {
   g_tune[kTuneSf32].store(env_int("MTP_SF32", -1), std::memory_order_relaxed);
   g_tune[kTuneSkpH8].store(env_int("MTP_SKP_H8", -1), std::memory_order_relaxed);
   g_tune[kTuneAttn32].store(env_int("MTP_ATTN32", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkXraw].store(env_int("MTP_SK_XRAW", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -372,9 +373,9 @@ int launch_wsp(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
 struct PlanSk {
   bool ok = false;
   int ct = 0, wt = 0, mt = 0;
-  bool gam = false;
+  bool gam = false, xr = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
-  size_t xf_off = 0, part_off = 0, total = 0;
+  size_t xf_off = 0, part_off = 0, ss_off = 0, total = 0;
 };
 
 // aim for most of the CUs busy (200 of 256)
@@ -382,7 +383,11 @@ int sk_min_blocks() { return device_cus() * 200 / 256; }
 constexpr int kSkMinStages = 4;    // stages per split at least
 
 // Tile: 64 columns x all rows of x (<= 64); K-splits only while the grid is
-// short of CUs. Workspace: counters, the xn blocks, split-K partials.
+// short of CUs. Without gamma and with one x tile the GEMM reads the raw x
+// rows and applies rs to its fp32 sums (no prep launch; tuning key sk_xraw
+// 1 forces it for two tiles, 0 keeps the prep).
+// Workspace: counters, the xn blocks (prep form), split-K partials (and the
+// splits' sums of squares in the raw form).
 PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   PlanSk p;
   p.ct = ct;
@@ -402,6 +407,11 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   if ((int64_t)kSkBN * K * wb >= (int64_t)1 << 31 || (int64_t)sk_xf_bytes(M, K) >= (int64_t)1 << 31)
     return p;
   p.mt = M <= 32 ? 1 : 2;
+  // raw x by default for one x tile: its 32-byte row segments cost less than
+  // the prep launch at <= 32 rows (bf16 32 x 4096 x 4096 12.7 us against
+  // 14.5, fp8 24 x 4096 x 4096 11.8 against 13.5), more at 64 rows (fp8
+  // 64 x 14336 x 4096 27.5 against 25.5)
+  p.xr = !gam && (tune(kTuneSkXraw) == 1 || (tune(kTuneSkXraw) != 0 && p.mt == 1));
   p.G = (int)((N + kSkBN - 1) / kSkBN);
   p.nkb = (int)(K * wb / kSkUB);
   int S = 1;
@@ -416,37 +426,52 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   if ((int64_t)p.G * p.S > INT32_MAX) return p;
   if (p.S > 1 && p.G > kCounterSlots) return p;
   size_t off = kCounterBytes;
-  p.xf_off = off;
-  off += align_up(sk_xf_bytes(M, K), 256);
+  if (!p.xr) {
+    p.xf_off = off;
+    off += align_up(sk_xf_bytes(M, K), 256);
+  }
   if (p.S > 1) {
     const size_t part = (size_t)p.S * p.G * sk_tile_bytes(p.mt);
     if (part >= ((size_t)1 << 31)) return p;
     p.part_off = off;
     off += align_up(part, 256);
+    if (p.xr) {
+      p.ss_off = off;
+      off += align_up((size_t)p.S * p.G * 64 * sizeof(float), 256);
+    }
   }
   p.total = off;
-  p.ok = sk_pick(ct, wt, p.mt) != nullptr && sk_prep_pick(ct, wt, gam) != nullptr;
+  p.ok = sk_pick(ct, wt, p.mt, p.xr) != nullptr &&
+         (p.xr || sk_prep_pick(ct, wt, gam) != nullptr);
   return p;
 }
 
 int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int norm,
               SkArgs &a, void *ws, hipStream_t st) {
-  SkKernel k = sk_pick(p.ct, p.wt, p.mt);
-  SkPrepKernel pk = sk_prep_pick(p.ct, p.wt, p.gam);
-  if (!k || !pk) return MTP_ERR_DTYPE;
+  SkKernel k = sk_pick(p.ct, p.wt, p.mt, p.xr);
+  if (!k) return MTP_ERR_DTYPE;
   unsigned char *w8 = (unsigned char *)ws;
-  SkPrepArgs pa;
-  pa.x = x;
-  pa.gamma = gamma;
-  pa.xf = w8 + p.xf_off;
-  pa.M = a.M;
-  pa.K = a.K;
-  pa.norm = norm;
-  pa.eps = eps;
-  hipLaunchKernelGGL(pk, dim3((unsigned)(32 * p.mt)), dim3(256), 0, st, pa);
-  int s = launch_status();
-  if (s != MTP_OK) return s;
-  a.xf = pa.xf;
+  if (p.xr) {
+    a.x = x;
+    a.norm = norm;
+    a.eps = eps;
+    if (p.S > 1) a.part_ss = (float *)(w8 + p.ss_off);
+  } else {
+    SkPrepKernel pk = sk_prep_pick(p.ct, p.wt, p.gam);
+    if (!pk) return MTP_ERR_DTYPE;
+    SkPrepArgs pa;
+    pa.x = x;
+    pa.gamma = gamma;
+    pa.xf = w8 + p.xf_off;
+    pa.M = a.M;
+    pa.K = a.K;
+    pa.norm = norm;
+    pa.eps = eps;
+    hipLaunchKernelGGL(pk, dim3((unsigned)(32 * p.mt)), dim3(256), 0, st, pa);
+    int s = launch_status();
+    if (s != MTP_OK) return s;
+    a.xf = pa.xf;
+  }
   a.G = p.G;
   a.S = p.S;
   a.kb_per = p.kb_per;

@@ -4,19 +4,19 @@
 namespace mtp {
 
 template <int CT, int WT>
-SkKernel sk_pick_w(int mt) {
-  if (mt == 1) return sk_kernel<CT, WT, 1>;
-  if (mt == 2) return sk_kernel<CT, WT, 2>;
+SkKernel sk_pick_w(int mt, bool xr) {
+  if (mt == 1) return xr ? sk_kernel<CT, WT, 1, true> : sk_kernel<CT, WT, 1, false>;
+  if (mt == 2) return xr ? sk_kernel<CT, WT, 2, true> : sk_kernel<CT, WT, 2, false>;
   return nullptr;
 }
 
-SkKernel sk_pick(int ct, int wt, int mt) {
+SkKernel sk_pick(int ct, int wt, int mt, bool xr) {
   if (ct == MTP_BF16) {
-    if (wt == MTP_FP8E4M3) return sk_pick_w<MTP_BF16, MTP_FP8E4M3>(mt);
-    if (wt == MTP_BF16) return sk_pick_w<MTP_BF16, MTP_BF16>(mt);
+    if (wt == MTP_FP8E4M3) return sk_pick_w<MTP_BF16, MTP_FP8E4M3>(mt, xr);
+    if (wt == MTP_BF16) return sk_pick_w<MTP_BF16, MTP_BF16>(mt, xr);
   } else if (ct == MTP_F16) {
-    if (wt == MTP_FP8E4M3) return sk_pick_w<MTP_F16, MTP_FP8E4M3>(mt);
-    if (wt == MTP_F16) return sk_pick_w<MTP_F16, MTP_F16>(mt);
+    if (wt == MTP_FP8E4M3) return sk_pick_w<MTP_F16, MTP_FP8E4M3>(mt, xr);
+    if (wt == MTP_F16) return sk_pick_w<MTP_F16, MTP_F16>(mt, xr);
   }
   return nullptr;
 }

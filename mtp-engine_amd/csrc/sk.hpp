@@ -172,8 +172,13 @@ sk_prep_kernel(const SkPrepArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. GEMM
-template <int CT, int WT, int MT>
+// 2. GEMM. XR (raw x, no gamma): the B operands come straight from the
+// caller's row-major x rows (16 contiguous bytes per lane: row 32 t +
+// lane % 32, the k-slots of its lane group), the sums of squares of the
+// rows come from one extra MFMA per x tile and k-step with the fragment as
+// both operands (the diagonal of x x^T), and rs multiplies the fp32 sums in
+// the epilogue: no prep launch.
+template <int CT, int WT, int MT, bool XR>
 __global__ void __launch_bounds__(256, 1)
 sk_kernel(const SkArgs a) {
   constexpr bool FP8 = WT == MTP_FP8E4M3;
@@ -189,6 +194,8 @@ sk_kernel(const SkArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * STAGE > RED ? 2 * STAGE : RED];
   static_assert((NS - 1) * NV < 64, "vmcnt is 6 bits");
   __shared__ int s_flag;
+  __shared__ float s_sq[4][XR ? 64 : 1];  // XR: each wave's row sums of squares
+  __shared__ float s_rs[XR ? 64 : 1];     // XR: row scales
 
   const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
   const int N = a.N, K = a.K;
@@ -221,12 +228,22 @@ sk_kernel(const SkArgs a) {
   }
   // xn load i = t * KPW + jj of the wave: tile t, k-step wave * KPW + jj
   const int nst_all = a.nkb;
-  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xf, (uint32_t)(MT * nst_all * KS) * 1024u);
+  const __amdgpu_buffer_rsrc_t xrs =
+      XR ? make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 2u)
+         : make_rsrc(a.xf, (uint32_t)(MT * nst_all * KS) * 1024u);
   uint32_t xvo[NXL];
 #pragma unroll
   for (int i = 0; i < NXL; ++i) {
     const int t = i / KPW, j = wave * KPW + i % KPW;
-    xvo[i] = (uint32_t)(((t * nst_all + st0) * KS + j) * 1024 + lane * 16);
+    if constexpr (XR) {
+      // k-slots of k-step j, lane group g (the order the prep writes)
+      const int g = lane >> 5;
+      const int kin = FP8 ? 32 * (j >> 1) + 16 * g + 8 * (j & 1) : 16 * j + 8 * g;
+      // rows >= M fall past the descriptor (zeros)
+      xvo[i] = (uint32_t)(((32 * t + (lane & 31)) * K + st0 * UK + kin) * 2);
+    } else {
+      xvo[i] = (uint32_t)(((t * nst_all + st0) * KS + j) * 1024 + lane * 16);
+    }
   }
   u32x4 xr[NS][NXL];   // xn register ring
   u32x4 wr[NS][NWC];   // W register ring
@@ -250,8 +267,8 @@ sk_kernel(const SkArgs a) {
     } else {
       constexpr int i = v - NWC;
       xr[slot][i] = __builtin_bit_cast(
-          u32x4,
-          __builtin_amdgcn_raw_buffer_load_b128(xrs, live ? xvo[i] : kOOB, str * KS * 1024, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, live ? xvo[i] : kOOB,
+                                                       XR ? str * UK * 2 : str * KS * 1024, 0));
     }
   };
 
@@ -262,6 +279,11 @@ sk_kernel(const SkArgs a) {
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[u][t][e] = 0.f;
+  f32x16 sq[XR ? MT : 1];  // XR: x x^T of each tile over this wave's k-steps
+#pragma unroll
+  for (int t = 0; t < (XR ? MT : 1); ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sq[t][e] = 0.f;
 
   // This wave's k-steps of a stage (A from W rows 32 u + lane % 32, B from
   // the xn blocks), with the copies of stage `nst_` spread over them.
@@ -303,6 +325,7 @@ sk_kernel(const SkArgs a) {
         const u32x4 bv = xr[slot][t * KPW + jj];
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[u][t] = mfma32<CT>(av[u], bv, acc[u][t]);
+        if constexpr (XR) sq[t] = mfma32<CT>(bv, bv, sq[t]);
       }
     });
   };
@@ -341,6 +364,22 @@ sk_kernel(const SkArgs a) {
   });
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last stage
   __syncthreads();
+  if constexpr (XR) {
+    // diagonal of x x^T: lane l (column j = l % 32) holds row i = 8 (v / 4)
+    // + 4 (l / 32) + v % 4 in slot v, so row j sits in the lane half
+    // (j / 4) % 2, slot 4 (j / 8) + j % 4
+    const int jr = lane & 31;
+    if ((lane >> 5) == ((jr >> 2) & 1)) {
+      const int vs = 4 * (jr >> 3) + (jr & 3);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        float d = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) d = v == vs ? sq[t][v] : d;
+        s_sq[wave][32 * t + jr] = d;
+      }
+    }
+  }
 
   // ---- the four waves' partial tiles meet in LDS: wave w sums output tile
   // (u, t) = (w % 2, w / 2) (waves past the MT tiles only contribute)
@@ -373,9 +412,11 @@ sk_kernel(const SkArgs a) {
 
   // lane's outputs: v[e] = D[n][m], m = 32 ot + lane % 32,
   // n = n0 + 32 ou + 8 (e / 4) + 4 (lane / 32) + e % 4
-  auto finish = [&](const f32x16 &r) {
+  auto finish = [&](const f32x16 &r0) {
     const int m = 32 * ot + (lane & 31);
     if (m >= a.M) return;
+    f32x16 r = r0;
+    if constexpr (XR) r *= s_rs[m];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = n0 + 32 * ou + 8 * g + 4 * ag;
@@ -397,7 +438,20 @@ sk_kernel(const SkArgs a) {
     }
   };
 
+  // XR: this workgroup's sums of squares of row th (its k-range, the four
+  // waves in order)
+  float ssw = 0.f;
+  if constexpr (XR) {
+    if (th < 32 * MT) ssw = ((s_sq[0][th] + s_sq[1][th]) + s_sq[2][th]) + s_sq[3][th];
+  }
+  auto set_rs = [&](float ss) {
+    if (th < 32 * MT) s_rs[th] = a.norm ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
+  };
   if (a.S == 1) {
+    if constexpr (XR) {
+      set_rs(ssw);
+      __syncthreads();
+    }
     if (owner) finish(v);
     return;
   }
@@ -419,11 +473,32 @@ sk_kernel(const SkArgs a) {
                                              part_off(sp, g4), 0, kSc1);
     }
   }
+  // XR: the split's sums of squares, [tile][split][64 rows]
+  const __amdgpu_buffer_rsrc_t qrs =
+      make_rsrc(a.part_ss, XR ? (uint32_t)(a.S * a.G) * 256u : 0u);
+  if constexpr (XR) {
+    if (th < 32 * MT)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ssw), qrs,
+                                            ((uint32_t)(tile * a.S + sp) * 64u + th) * 4u, 0, kSc1);
+  }
   wait_stores();
   __syncthreads();
   if (th == 0) s_flag = (ticket_add(a.ticket + tile) == (unsigned)(a.S - 1));
   __syncthreads();
   if (!s_flag) return;
+  if constexpr (XR) {
+    // every split's sums of row th in split order (own term from registers)
+    float ss = 0.f;
+    if (th < 32 * MT) {
+      for (int q = 0; q < a.S; ++q)
+        ss += q == sp ? ssw
+                      : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      qrs, ((uint32_t)(tile * a.S + q) * 64u + th) * 4u,
+                                                      0, kSc1));
+    }
+    set_rs(ss);
+    __syncthreads();
+  }
   if (owner) {
     // sums in split order (its own term from registers); the loads of QB
     // splits go out together, one round trip for up to QB splits

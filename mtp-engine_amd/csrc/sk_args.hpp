@@ -21,6 +21,10 @@ struct SkPrepArgs {
 
 struct SkArgs {
   const void *xf;       // xn blocks written by the prep
+  const void *x;        // raw x rows [M, K] (the prep-free form, no gamma)
+  int norm;             // raw form: apply rs
+  float eps;
+  float *part_ss;       // raw form with split-K: sums of squares [G][S][64]
   const void *w;        // [N, K] fp8 or compute type
   const float *wscale;  // [N] or null
   const void *bias;     // [N] or null
@@ -35,9 +39,9 @@ struct SkArgs {
 
 typedef void (*SkKernel)(SkArgs);
 typedef void (*SkPrepKernel)(SkPrepArgs);
-// GEMM for x dtype ct (BF16 / F16), W dtype wt (FP8E4M3 or ct) and mt
-// 32-row tiles of x (1 or 2), or null.
-SkKernel sk_pick(int ct, int wt, int mt);
+// GEMM for x dtype ct (BF16 / F16), W dtype wt (FP8E4M3 or ct), mt 32-row
+// tiles of x (1 or 2), reading the prep's xn blocks or (xr) raw x, or null.
+SkKernel sk_pick(int ct, int wt, int mt, bool xr);
 // Prep for x dtype ct, the k-slot order of W dtype wt, gamma present, or null.
 SkPrepKernel sk_prep_pick(int ct, int wt, bool gam);
 

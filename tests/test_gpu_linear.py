@@ -163,7 +163,9 @@ def test_fp8_tile_variants_and_splits(tune, M, xdtype):
 def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
     """The skinny weight-streaming kernel (M <= 64, 16-bit x, fp8 or 16-bit
     W): every forced K-split count, ragged M and N, with and without gamma
-    and norm, against the oracle."""
+    and norm, against the oracle. Without gamma it can read the raw x rows
+    and apply rs to the fp32 sums (no prep launch; sk_xraw=1 forces it); the
+    prep form (sk_xraw=0) gives the oracle's answer on the same inputs too."""
     _set(sk_splits=int(splits))
     from mtp_hip import ops
     print(f"case splits={splits} M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
@@ -188,6 +190,23 @@ def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
     for out, r in ((y, ref), (y2, ref2)):
         ok, worst = close(out, r, 2e-2)
         assert ok, f"worst err/bound = {worst:.3g}"
+    # no gamma, norm and bias: the raw-x form (forced: also for two x
+    # tiles), then the prep form
+    for xraw in (1, 0):
+        _set(sk_xraw=xraw)
+        if wkind == "fp8":
+            y3 = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6)
+            ref3 = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6)
+        else:
+            y3 = ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5)
+            ref3 = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5)
+        torch.cuda.synchronize()
+        ok, worst = close(y3, ref3, 2e-2)
+        assert ok, f"sk_xraw={xraw}: worst err/bound = {worst:.3g}"
+        if xraw == 1:
+            assert torch.equal(y3, ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6)
+                               if wkind == "fp8" else
+                               ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5))
 
 
 SKL_CASES = [(None, "8", (40, 40000, 512)), (None, "8", (3, 33024, 256)),
