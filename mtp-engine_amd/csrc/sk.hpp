@@ -490,11 +490,23 @@ sk_kernel(const SkArgs a) {
     // every split's sums of row th in split order (own term from registers)
     float ss = 0.f;
     if (th < 32 * MT) {
-      for (int q = 0; q < a.S; ++q)
-        ss += q == sp ? ssw
-                      : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                      qrs, ((uint32_t)(tile * a.S + q) * 64u + th) * 4u,
-                                                      0, kSc1));
+      // four splits' loads together per round trip
+      for (int q0 = 0; q0 < a.S; q0 += 4) {
+        float pv[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int q = q0 + qq;
+          const bool ld = q < a.S && q != sp;
+          pv[qq] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(
+                         qrs, ld ? ((uint32_t)(tile * a.S + q) * 64u + th) * 4u : kOOB, 0, kSc1));
+        }
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int q = q0 + qq;
+          if (q < a.S) ss += q == sp ? ssw : pv[qq];
+        }
+      }
     }
     set_rs(ss);
     __syncthreads();
