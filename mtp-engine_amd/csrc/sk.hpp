@@ -172,12 +172,13 @@ sk_prep_kernel(const SkPrepArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. GEMM. XR (raw x, no gamma): the B operands come straight from the
-// caller's row-major x rows (16 contiguous bytes per lane: row 32 t +
-// lane % 32, the k-slots of its lane group), the sums of squares of the
-// rows come from one extra MFMA per x tile and k-step with the fragment as
-// both operands (the diagonal of x x^T), and rs multiplies the fp32 sums in
-// the epilogue: no prep launch.
+// 2. GEMM. XR (raw x, no gamma): the caller's row-major x rows come in with
+// the W loads' pattern (8 rows x 128 contiguous bytes per instruction) and
+// go to LDS B-operand blocks beside W one stage before use (lane 32 g + m
+// of block (tile, k-step j) at slot (32 g + m) ^ sk_xswz(j, g)); the sums of
+// squares of the rows come from one extra MFMA per x tile and k-step with
+// the B fragment as both operands (the diagonal of x x^T), and rs
+// multiplies the fp32 sums in the epilogue: no prep launch.
 template <int CT, int WT, int MT, bool XR>
 __global__ void __launch_bounds__(256, 1)
 sk_kernel(const SkArgs a) {
@@ -194,6 +195,8 @@ sk_kernel(const SkArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * STAGE > RED ? 2 * STAGE : RED];
   static_assert((NS - 1) * NV < 64, "vmcnt is 6 bits");
   __shared__ int s_flag;
+  constexpr int XST = MT * KS * 1024;      // XR: x B-operand bytes of one stage
+  __shared__ __attribute__((aligned(1024))) unsigned char ldsx[XR ? 2 * XST : 16];
   __shared__ float s_sq[4][XR ? 64 : 1];  // XR: each wave's row sums of squares
   __shared__ float s_rs[XR ? 64 : 1];     // XR: row scales
 
@@ -232,16 +235,22 @@ sk_kernel(const SkArgs a) {
       XR ? make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 2u)
          : make_rsrc(a.xf, (uint32_t)(MT * nst_all * KS) * 1024u);
   uint32_t xvo[NXL];
+  int xl[XR ? NXL : 1];  // XR: LDS byte offset of load i's 16 bytes in a stage
 #pragma unroll
   for (int i = 0; i < NXL; ++i) {
-    const int t = i / KPW, j = wave * KPW + i % KPW;
     if constexpr (XR) {
-      // k-slots of k-step j, lane group g (the order the prep writes)
-      const int g = lane >> 5;
-      const int kin = FP8 ? 32 * (j >> 1) + 16 * g + 8 * (j & 1) : 16 * j + 8 * g;
-      // rows >= M fall past the descriptor (zeros)
-      xvo[i] = (uint32_t)(((32 * t + (lane & 31)) * K + st0 * UK + kin) * 2);
+      // load c = wave + 4 i: rows 8 (c mod 4 MT) + lane / 8 (rows >= M fall
+      // past the descriptor: zeros), 16-byte piece q = 8 (c / 4 MT) + lane % 8
+      // of the row's UK k of the stage
+      const int c = wave + 4 * i;
+      const int row = 8 * (c % (4 * MT)) + (lane >> 3);
+      const int q = 8 * (c / (4 * MT)) + (lane & 7);
+      int j, g;
+      sk_chunk_slot<FP8>(q, j, g);
+      xvo[i] = (uint32_t)((row * K + st0 * UK) * 2 + 16 * q);
+      xl[i] = (((row >> 5) * KS + j) * 64 + ((32 * g + (row & 31)) ^ sk_xswz(j, g))) * 16;
     } else {
+      const int t = i / KPW, j = wave * KPW + i % KPW;
       xvo[i] = (uint32_t)(((t * nst_all + st0) * KS + j) * 1024 + lane * 16);
     }
   }
@@ -294,6 +303,10 @@ sk_kernel(const SkArgs a) {
 #pragma unroll
     for (int v = 0; v < NWC; ++v)
       *(u32x4 *)(lds + b * STAGE + (wave + 4 * v) * 1024 + lane * 16) = wr[slot][v];
+    if constexpr (XR) {
+#pragma unroll
+      for (int i = 0; i < NXL; ++i) *(u32x4 *)(ldsx + b * XST + xl[i]) = xr[slot][i];
+    }
   };
   auto compute = [&](auto slotc, int nst_, auto nslotc) __attribute__((always_inline)) {
     constexpr int slot = decltype(slotc)::value;
@@ -322,7 +335,10 @@ sk_kernel(const SkArgs a) {
       }
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const u32x4 bv = xr[slot][t * KPW + jj];
+        const u32x4 bv =
+            XR ? *(const u32x4 *)(ldsx + (slot & 1) * XST + (t * KS + j) * 1024 +
+                                  ((lane ^ sk_xswz(j, ag)) << 4))
+               : xr[slot][t * KPW + jj];
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[u][t] = mfma32<CT>(av[u], bv, acc[u][t]);
         if constexpr (XR) sq[t] = mfma32<CT>(bv, bv, sq[t]);
