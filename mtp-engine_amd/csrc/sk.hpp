@@ -112,7 +112,12 @@ __global__ void __launch_bounds__(256)
 sk_prep_kernel(const SkPrepArgs a) {
   constexpr int UK = FP8 ? 128 : 64, KS = UK / 16, QPS = UK / 8;
   __shared__ float red[4];
-  const int m = blockIdx.x, th = threadIdx.x;
+  // 64-row grids: the 8 rows sharing the 128-byte lines of the xn blocks go
+  // to blocks of one XCD (b mod 8), so their 16-byte stores meet in one L2
+  // and leave as whole lines (bf16 64 x 14336 x 4096: 31.2 -> 30.6 us per
+  // call); any block order gives the same result
+  const int b = blockIdx.x, th = threadIdx.x;
+  const int m = gridDim.x % 64 == 0 ? 8 * (8 * ((b >> 3) >> 3) + (b & 7)) + ((b >> 3) & 7) : b;
   const int K = a.K, nst = K / UK;
   u32x4 *xf = (u32x4 *)a.xf;
   // block (tile, stage, k-step) is 1 KB = 64 lanes of 16 bytes
