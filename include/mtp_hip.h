@@ -84,9 +84,8 @@ const char *mtp_last_hip_error(void);
  * disable the x-resident skinny kernel), "skp_splits", "skp_ta" (A tiles
  * per wave: 1, 2 or 4), "skp_h8" (0: full x blocks in the x-resident
  * kernel for at most 8 rows), "sf32" (0: no small fp32 kernel), "attn32"
- * (0: 16-query-tile attention for 33 .. 64 queries), "sk_xraw" (1: the
- * skinny kernel reads raw x rows without gamma also for fp8 W at 33 .. 64
- * rows, 0: never). value -1 restores the
+ * (0: 16-query-tile attention for 33 .. 64 queries), "sk_xraw" (0: the
+ * skinny kernel keeps its prep launch without gamma too). value -1 restores the
  * planner's choice. The MTP_SKL, MTP_SK_SPLITS, MTP_WS_TUNE
  * ("variant,splits"), MTP_SKL_WAVES, MTP_SKL_SPLITS, MTP_ATTN_CHUNK_BLOCKS,
  * MTP_INT4_WAVES, MTP_VERIFY_WSTREAM, MTP_SKP, MTP_SKP_SPLITS, MTP_SKP_TA,

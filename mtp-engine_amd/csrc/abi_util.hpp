@@ -56,7 +56,7 @@ enum TuneKey {
   kTuneSf32,             // MTP_SF32: small fp32 kernel, 0 off (default on where it applies)
   kTuneSkpH8,            // MTP_SKP_H8: compact x blocks of the x-resident kernel (<= 8 rows), 0 off
   kTuneAttn32,           // MTP_ATTN32: 32-query-tile attention (33 .. 64 queries, D 128), 0 off
-  kTuneSkXraw,           // MTP_SK_XRAW: sk reads raw x without gamma (no prep launch): 1 force, 0 off
+  kTuneSkXraw,           // MTP_SK_XRAW: 0 keeps sk's prep launch without gamma (default: raw x)
   kTuneCount
 };
 int tune(TuneKey k);

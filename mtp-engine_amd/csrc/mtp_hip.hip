@@ -384,8 +384,7 @@ constexpr int kSkMinStages = 4;    // stages per split at least
 
 // Tile: 64 columns x all rows of x (<= 64); K-splits only while the grid is
 // short of CUs. Without gamma the GEMM reads the raw x rows and applies rs
-// to its fp32 sums (no prep launch; not for fp8 W with two x tiles; tuning
-// key sk_xraw 1 forces it, 0 keeps the prep).
+// to its fp32 sums (no prep launch; tuning key sk_xraw 0 keeps the prep).
 // Workspace: counters, the xn blocks (prep form), split-K partials (and the
 // splits' sums of squares in the raw form).
 PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
@@ -407,12 +406,10 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   if ((int64_t)kSkBN * K * wb >= (int64_t)1 << 31 || (int64_t)sk_xf_bytes(M, K) >= (int64_t)1 << 31)
     return p;
   p.mt = M <= 32 ? 1 : 2;
-  // raw x by default except fp8 W with two x tiles, where staging 16 KB of
-  // x per stage beside W costs more than the prep launch saves (fp8 64 x
-  // 14336 x 4096: 27.6 us against 25.6; bf16 64 x 4096 x 4096: 14.9
-  // against 16.3; bf16 32 x 4096 x 4096: 12.2 against 14.5)
-  p.xr = !gam && (tune(kTuneSkXraw) == 1 ||
-                  (tune(kTuneSkXraw) != 0 && (p.mt == 1 || wt != MTP_FP8E4M3)));
+  // raw x whenever there is no gamma (bf16 64 x 4096 x 4096: 14.5 us
+  // against 16.3 with the prep; bf16 32 x 4096 x 4096: 12.0 against 14.5;
+  // fp8 64 x 14336 x 4096: 25.1 either way)
+  p.xr = !gam && tune(kTuneSkXraw) != 0;
   p.G = (int)((N + kSkBN - 1) / kSkBN);
   p.nkb = (int)(K * wb / kSkUB);
   int S = 1;

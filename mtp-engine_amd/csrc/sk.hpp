@@ -181,9 +181,23 @@ sk_prep_kernel(const SkPrepArgs a) {
 // the W loads' pattern (8 rows x 128 contiguous bytes per instruction) and
 // go to LDS B-operand blocks beside W one stage before use (lane 32 g + m
 // of block (tile, k-step j) at slot (32 g + m) ^ sk_xswz(j, g)); the sums of
-// squares of the rows come from one extra MFMA per x tile and k-step with
-// the B fragment as both operands (the diagonal of x x^T), and rs
-// multiplies the fp32 sums in the epilogue: no prep launch.
+// squares of the rows are taken on the way to LDS (v_dot2 of each 16-byte
+// piece with itself, fp32 sums; every row's pieces arrive in one wave, so a
+// row's sum needs only the 8 lanes that hold it), and rs multiplies the
+// fp32 sums in the epilogue: no prep launch.
+template <int CT>
+__device__ __forceinline__ float sk_sumsq2(uint32_t v, float acc) {
+  if constexpr (CT == MTP_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v),
+                                           __builtin_bit_cast(bf16x2_t, v), acc, false);
+  } else {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, v), __builtin_bit_cast(f16x2_t, v),
+                                  acc, false);
+  }
+}
+
 template <int CT, int WT, int MT, bool XR>
 __global__ void __launch_bounds__(256, 1)
 sk_kernel(const SkArgs a) {
@@ -202,7 +216,7 @@ sk_kernel(const SkArgs a) {
   __shared__ int s_flag;
   constexpr int XST = MT * KS * 1024;      // XR: x B-operand bytes of one stage
   __shared__ __attribute__((aligned(1024))) unsigned char ldsx[XR ? 2 * XST : 16];
-  __shared__ float s_sq[4][XR ? 64 : 1];  // XR: each wave's row sums of squares
+  __shared__ float s_sq[XR ? 64 : 1];     // XR: row sums of squares (this k-range)
   __shared__ float s_rs[XR ? 64 : 1];     // XR: row scales
 
   const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
@@ -293,11 +307,11 @@ sk_kernel(const SkArgs a) {
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[u][t][e] = 0.f;
-  f32x16 sq[XR ? MT : 1];  // XR: x x^T of each tile over this wave's k-steps
+  // XR: the lane's sums of squares of rows 8 (w + 4 t) + lane / 8 (t < MT:
+  // x load i covers rows 8 ((w + 4 i) mod 4 MT) + lane / 8, so t = i mod MT)
+  float ssl[XR ? MT : 1];
 #pragma unroll
-  for (int t = 0; t < (XR ? MT : 1); ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sq[t][e] = 0.f;
+  for (int t = 0; t < (XR ? MT : 1); ++t) ssl[t] = 0.f;
 
   // This wave's k-steps of a stage (A from W rows 32 u + lane % 32, B from
   // the xn blocks), with the copies of stage `nst_` spread over them.
@@ -310,7 +324,11 @@ sk_kernel(const SkArgs a) {
       *(u32x4 *)(lds + b * STAGE + (wave + 4 * v) * 1024 + lane * 16) = wr[slot][v];
     if constexpr (XR) {
 #pragma unroll
-      for (int i = 0; i < NXL; ++i) *(u32x4 *)(ldsx + b * XST + xl[i]) = xr[slot][i];
+      for (int i = 0; i < NXL; ++i) {
+        *(u32x4 *)(ldsx + b * XST + xl[i]) = xr[slot][i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ssl[i % MT] = sk_sumsq2<CT>(xr[slot][i][e], ssl[i % MT]);
+      }
     }
   };
   auto compute = [&](auto slotc, int nst_, auto nslotc) __attribute__((always_inline)) {
@@ -346,7 +364,6 @@ sk_kernel(const SkArgs a) {
                : xr[slot][t * KPW + jj];
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[u][t] = mfma32<CT>(av[u], bv, acc[u][t]);
-        if constexpr (XR) sq[t] = mfma32<CT>(bv, bv, sq[t]);
       }
     });
   };
@@ -386,19 +403,14 @@ sk_kernel(const SkArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last stage
   __syncthreads();
   if constexpr (XR) {
-    // diagonal of x x^T: lane l (column j = l % 32) holds row i = 8 (v / 4)
-    // + 4 (l / 32) + v % 4 in slot v, so row j sits in the lane half
-    // (j / 4) % 2, slot 4 (j / 8) + j % 4
-    const int jr = lane & 31;
-    if ((lane >> 5) == ((jr >> 2) & 1)) {
-      const int vs = 4 * (jr >> 3) + (jr & 3);
+    // the 8 lanes of each row (lane / 8), then one store per row
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        float d = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) d = v == vs ? sq[t][v] : d;
-        s_sq[wave][32 * t + jr] = d;
-      }
+    for (int t = 0; t < MT; ++t) {
+      float v = ssl[t];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      if ((lane & 7) == 0) s_sq[8 * (wave + 4 * t) + (lane >> 3)] = v;
     }
   }
 
@@ -459,11 +471,10 @@ sk_kernel(const SkArgs a) {
     }
   };
 
-  // XR: this workgroup's sums of squares of row th (its k-range, the four
-  // waves in order)
+  // XR: this workgroup's sums of squares of row th (its k-range)
   float ssw = 0.f;
   if constexpr (XR) {
-    if (th < 32 * MT) ssw = ((s_sq[0][th] + s_sq[1][th]) + s_sq[2][th]) + s_sq[3][th];
+    if (th < 32 * MT) ssw = s_sq[th];
   }
   auto set_rs = [&](float ss) {
     if (th < 32 * MT) s_rs[th] = a.norm ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;

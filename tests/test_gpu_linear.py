@@ -164,8 +164,9 @@ def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
     """The skinny weight-streaming kernel (M <= 64, 16-bit x, fp8 or 16-bit
     W): every forced K-split count, ragged M and N, with and without gamma
     and norm, against the oracle. Without gamma it can read the raw x rows
-    and apply rs to the fp32 sums (no prep launch; sk_xraw=1 forces it); the
-    prep form (sk_xraw=0) gives the oracle's answer on the same inputs too."""
+    and apply rs to the fp32 sums (no prep launch; the default, sk_xraw=1);
+    the prep form (sk_xraw=0) gives the oracle's answer on the same inputs
+    too."""
     _set(sk_splits=int(splits))
     from mtp_hip import ops
     print(f"case splits={splits} M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
