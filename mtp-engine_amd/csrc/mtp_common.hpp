@@ -229,6 +229,21 @@ __device__ __forceinline__ int get_i32(const int *p) {
 }
 // Every thread: wait for its own stores/atomics to complete.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+// Split-K grid of G column tiles x S splits: (tile, split) of block b. With
+// xg and G % 8 == 0 the S splits of a tile are blocks of one XCD (blocks
+// are dealt to the 8 XCDs as b mod 8), so a tile's hand-off and arrival
+// ticket stay on one XCD; otherwise the splits of a tile are consecutive
+// blocks. Any bijection gives the same result.
+__device__ __forceinline__ void split_tile_of(int b, int G, int S, bool xg, int &tile, int &sp) {
+  if (xg && S > 1 && (G & 7) == 0) {
+    const int r = b >> 3, t8 = r / S;
+    tile = 8 * t8 + (b & 7);
+    sp = r - t8 * S;
+  } else {
+    tile = b / S;
+    sp = b - tile * S;
+  }
+}
 // Arrival count at the coherence point (returns the previous value).
 __device__ __forceinline__ unsigned ticket_add(unsigned *t) {
   return __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -562,6 +562,10 @@ int launch_skl(const PlanSkl &p, SklArgs &a, void *ws, hipStream_t st) {
   a.S = p.S;
   a.kb_per = p.kb_per;
   a.nkb = p.nkb;
+  // the splits of a tile on one XCD from 4 splits up (fp8 24 x 14336 x
+  // 4096: 19.1 -> 17.6 us); with 2 splits it loses (fp8 64 x 28672 x 4096:
+  // 38.4 -> 39.9 us)
+  a.xg = p.S >= 4;
   if (p.S > 1) {
     a.part = (float *)(w8 + p.part_off);
     a.part_ss = (float *)(w8 + p.ss_off);
@@ -672,6 +676,10 @@ int launch_skp(const PlanSkp &p, SkpArgs &a, void *ws, hipStream_t st) {
   a.S = p.S;
   a.kb_per = p.kb_per;
   a.nkb = p.nkb;
+  // the splits of a tile on one XCD with compact x blocks (fp8 8 x 4096 x
+  // 4096: 10.3 -> 9.5 us); with full blocks it loses (bf16 16 x 4096 x
+  // 4096: 11.1 -> 11.4 us)
+  a.xg = p.h8 ? 1 : 0;
   if (p.S > 1) {
     a.part = (float *)(w8 + p.part_off);
     a.part_ss = (float *)(w8 + p.ss_off);

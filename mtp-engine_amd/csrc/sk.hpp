@@ -222,8 +222,11 @@ sk_kernel(const SkArgs a) {
   const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
   const int N = a.N, K = a.K;
 
-  // blockIdx -> (column tile, split): the splits of a tile are consecutive
-  const int tile = (int)blockIdx.x / a.S, sp = (int)blockIdx.x - tile * a.S;
+  // blockIdx -> (column tile, split): the splits of a tile on one XCD
+  // (bf16 64 x 4096 x 4096, 4 splits: 14.5 -> 14.2 us; fp8 24 x 4096 x
+  // 4096: 11.5 -> 11.1 us)
+  int tile, sp;
+  split_tile_of((int)blockIdx.x, a.G, a.S, true, tile, sp);
   const int n0 = tile * kSkBN;
   // end-phase owner of this wave (see below) and its column factors
   const int ou = wave & 1, ot = wave >> 1;

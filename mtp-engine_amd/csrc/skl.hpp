@@ -81,7 +81,8 @@ skl_kernel(const SklArgs a) {
   const int ag = lane >> 5;
   const int N = a.N, K = a.K;
   const int b = blockIdx.x;
-  const int tile = b / a.S, sp = b - tile * a.S;
+  int tile, sp;
+  split_tile_of(b, a.G, a.S, a.xg != 0, tile, sp);
   const int n0 = tile * BN;
   const int st0 = sp * a.kb_per;
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // stages of this split (>= 1)

@@ -94,7 +94,8 @@ skp_kernel(const SkpArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
   const int N = a.N, K = a.K;
   const int b = blockIdx.x;
-  const int tile = b / a.S, sp = b - tile * a.S;
+  int tile, sp;
+  split_tile_of(b, a.G, a.S, a.xg != 0, tile, sp);
   const int n0 = tile * BN;
   const int st0 = sp * a.kb_per;
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // steps of this split (>= 1)
