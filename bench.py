@@ -344,8 +344,9 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE can be scaled to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build runs on a single MI355X and has no "
-              "multi-GPU path (see DESIGN.md for how the path would shard).", file=sys.stderr)
+        print("bench.py measures one GPU: the library runs on a single MI355X and has no "
+              "multi-GPU path (the verify kernels would shard the vocabulary columns across "
+              "GPUs, one process per GPU).", file=sys.stderr)
         sys.exit(2)
 
     import torch
