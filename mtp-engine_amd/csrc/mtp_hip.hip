@@ -375,7 +375,8 @@ struct PlanSk {
   int ct = 0, wt = 0, mt = 0;
   bool gam = false, xr = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
-  size_t xf_off = 0, part_off = 0, ss_off = 0, total = 0;
+  int ch = 1, nsl = 0;  // prep form: 256 ch k per prep slice, slices
+  size_t xf_off = 0, pss_off = 0, part_off = 0, ss_off = 0, total = 0;
 };
 
 // aim for most of the CUs busy (200 of 256)
@@ -401,7 +402,7 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   if (M <= 0 || M > 64 || N <= 0 || K <= 0 || (M <= 16 && !forced)) return p;
   if (tune(kTuneWsVariant) >= 0 || tune(kTuneWsSplits) > 0) return p;  // sweeps of wsp
   const int wb = dtype_bytes(wt);
-  if ((K * wb) % kSkUB != 0 || K > 256 * 8 * kSkPrepChunks) return p;
+  if ((K * wb) % kSkUB != 0 || K > kSkMaxK) return p;
   // buffer descriptors: the workgroup's W rows, all xn blocks
   if ((int64_t)kSkBN * K * wb >= (int64_t)1 << 31 || (int64_t)sk_xf_bytes(M, K) >= (int64_t)1 << 31)
     return p;
@@ -427,6 +428,14 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   if (!p.xr) {
     p.xf_off = off;
     off += align_up(sk_xf_bytes(M, K), 256);
+    // prep slices: 256 ch k each, at most kSkPrepMaxSlices of them
+    const int64_t nq = K / 8;
+    p.ch = 1;
+    while (p.ch < 4 && (nq + 32 * p.ch - 1) / (32 * p.ch) > kSkPrepMaxSlices) p.ch *= 2;
+    p.nsl = (int)((nq + 32 * p.ch - 1) / (32 * p.ch));
+    if (p.nsl > kSkPrepMaxSlices) return p;
+    p.pss_off = off;
+    off += align_up((size_t)kSkPrepMaxSlices * 64 * sizeof(float), 256);
   }
   if (p.S > 1) {
     const size_t part = (size_t)p.S * p.G * sk_tile_bytes(p.mt);
@@ -440,7 +449,7 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   }
   p.total = off;
   p.ok = sk_pick(ct, wt, p.mt, p.xr) != nullptr &&
-         (p.xr || sk_prep_pick(ct, wt, gam) != nullptr);
+         (p.xr || sk_prep8_pick(ct, wt, gam, p.ch) != nullptr);
   return p;
 }
 
@@ -455,7 +464,7 @@ int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int
     a.eps = eps;
     if (p.S > 1) a.part_ss = (float *)(w8 + p.ss_off);
   } else {
-    SkPrepKernel pk = sk_prep_pick(p.ct, p.wt, p.gam);
+    SkPrep8Kernel pk = sk_prep8_pick(p.ct, p.wt, p.gam, p.ch);
     if (!pk) return MTP_ERR_DTYPE;
     SkPrepArgs pa;
     pa.x = x;
@@ -465,10 +474,15 @@ int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int
     pa.K = a.K;
     pa.norm = norm;
     pa.eps = eps;
-    hipLaunchKernelGGL(pk, dim3((unsigned)(32 * p.mt)), dim3(256), 0, st, pa);
+    float *pss = (float *)(w8 + p.pss_off);
+    hipLaunchKernelGGL(pk, dim3((unsigned)(4 * p.mt), (unsigned)p.nsl), dim3(256), 0, st, pa, pss);
     int s = launch_status();
     if (s != MTP_OK) return s;
     a.xf = pa.xf;
+    a.pss = pss;
+    a.nsl = p.nsl;
+    a.norm = norm;
+    a.eps = eps;
   }
   a.G = p.G;
   a.S = p.S;

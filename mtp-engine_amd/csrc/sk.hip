@@ -21,15 +21,23 @@ SkKernel sk_pick(int ct, int wt, int mt, bool xr) {
   return nullptr;
 }
 
-template <int CT>
-SkPrepKernel sk_prep_ct(bool fp8, bool gam) {
-  if (fp8) return gam ? sk_prep_kernel<CT, true, true> : sk_prep_kernel<CT, true, false>;
-  return gam ? sk_prep_kernel<CT, false, true> : sk_prep_kernel<CT, false, false>;
+template <int CT, bool FP8, bool GAM>
+SkPrep8Kernel sk_prep8_c(int ch) {
+  if (ch == 1) return sk_prep8_kernel<CT, FP8, GAM, 1>;
+  if (ch == 2) return sk_prep8_kernel<CT, FP8, GAM, 2>;
+  if (ch == 4) return sk_prep8_kernel<CT, FP8, GAM, 4>;
+  return nullptr;
 }
 
-SkPrepKernel sk_prep_pick(int ct, int wt, bool gam) {
-  if (ct == MTP_BF16) return sk_prep_ct<MTP_BF16>(wt == MTP_FP8E4M3, gam);
-  if (ct == MTP_F16) return sk_prep_ct<MTP_F16>(wt == MTP_FP8E4M3, gam);
+template <int CT>
+SkPrep8Kernel sk_prep8_ct(bool fp8, bool gam, int ch) {
+  if (fp8) return gam ? sk_prep8_c<CT, true, true>(ch) : sk_prep8_c<CT, true, false>(ch);
+  return gam ? sk_prep8_c<CT, false, true>(ch) : sk_prep8_c<CT, false, false>(ch);
+}
+
+SkPrep8Kernel sk_prep8_pick(int ct, int wt, bool gam, int ch) {
+  if (ct == MTP_BF16) return sk_prep8_ct<MTP_BF16>(wt == MTP_FP8E4M3, gam, ch);
+  if (ct == MTP_F16) return sk_prep8_ct<MTP_F16>(wt == MTP_FP8E4M3, gam, ch);
   return nullptr;
 }
 

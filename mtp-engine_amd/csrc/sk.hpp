@@ -4,11 +4,13 @@
 //   y[m, n] = (xn[m, :] . W[n, :]) * wscale[n] + bias[n], times scale
 //   xn[m, k] = x[m, k] * rs[m] * gamma[k],  rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) (norm) or 1
 //
-// Two launches:
-//  1. sk_prep_kernel, one block per row of x (rows padded to whole 32-row
-//     tiles, padding rows zero): xn rounded to the MFMA input type (the type
-//     of x), written as the B operands of v_mfma_f32_32x32x16: for each
-//     32-row tile, stage and k-step, one 1 KB block of 64 lanes x 16 bytes.
+// Two launches (one without gamma: the raw-x form below):
+//  1. sk_prep8_kernel, blocks of 8 rows x one K-slice (rows padded to whole
+//     32-row tiles, padding rows zero): xg = x * gamma rounded to the MFMA
+//     input type (the type of x), written as the B operands of
+//     v_mfma_f32_32x32x16 (for each 32-row tile, stage and k-step, one 1 KB
+//     block of 64 lanes x 16 bytes), and each row's sum of squares per
+//     slice; the GEMM sums the slices and applies rs to its fp32 sums.
 //     Doing this once per launch instead of once per column group keeps the
 //     GEMM free of per-element vector work on x.
 //  2. sk_kernel: bound by reading W once from HBM. A "stage" is 128 bytes
@@ -105,75 +107,80 @@ __device__ __forceinline__ void sk_lds_copy16(__amdgpu_buffer_rsrc_t r, unsigned
 #endif
 }
 
+// 4 bytes per lane into LDS (lane i writes bytes 4 i .. 4 i + 3 after `lds`).
+__device__ __forceinline__ void sk_lds_copy4(__amdgpu_buffer_rsrc_t r, unsigned char *lds,
+                                             uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4,
+                                           voff, 0, 0, 0);
+#else
+  (void)r; (void)lds; (void)voff;
+#endif
+}
+
 // ---------------------------------------------------------------------------
-// 1. prep: row m of x -> xn blocks
-template <int CT, bool FP8, bool GAM>
+// 1. prep
+// Prep of 8 rows x one K-slice of 256 CH k per block (block (g, s): rows
+// 8 g .. 8 g + 7, chunks 32 CH s ..): xg = x * gamma rounded to the MFMA
+// type into the xn blocks, and each row's sum of squares over the slice
+// into ss[s][64]; the GEMM applies rs to its fp32 sums. Lane 8 c + r of a
+// wave holds row r of chunk c, so a load instruction reads 8 rows x 128
+// contiguous bytes and the 8 lanes of a chunk store one whole 128-byte line
+// of an xn block; gamma comes in the same round trip as x.
+template <int CT, bool FP8, bool GAM, int CH>
 __global__ void __launch_bounds__(256)
-sk_prep_kernel(const SkPrepArgs a) {
+sk_prep8_kernel(const SkPrepArgs a, float *pss) {
   constexpr int UK = FP8 ? 128 : 64, KS = UK / 16, QPS = UK / 8;
-  __shared__ float red[4];
-  // 64-row grids: the 8 rows sharing the 128-byte lines of the xn blocks go
-  // to blocks of one XCD (b mod 8), so their 16-byte stores meet in one L2
-  // and leave as whole lines (bf16 64 x 14336 x 4096: 31.2 -> 30.6 us per
-  // call); any block order gives the same result
-  const int b = blockIdx.x, th = threadIdx.x;
-  const int m = gridDim.x % 64 == 0 ? 8 * (8 * ((b >> 3) >> 3) + (b & 7)) + ((b >> 3) & 7) : b;
-  const int K = a.K, nst = K / UK;
-  u32x4 *xf = (u32x4 *)a.xf;
-  // block (tile, stage, k-step) is 1 KB = 64 lanes of 16 bytes
-  auto out = [&](int q_all) -> u32x4 & {
-    const int st = q_all / QPS, q = q_all - st * QPS;
-    int j, g;
-    sk_chunk_slot<FP8>(q, j, g);
-    return xf[(((int64_t)(m >> 5) * nst + st) * KS + j) * 64 + 32 * g + (m & 31)];
-  };
-  const int nq = K / 8;
-  if (m >= a.M) {
-    for (int q = th; q < nq; q += 256) out(q) = u32x4{0u, 0u, 0u, 0u};
-    return;
-  }
-  // the row is read once: up to kSkPrepChunks 16-byte chunks per thread
-  // stay in registers between the sum of squares and the scaling
-  const u32x4 *xr = (const u32x4 *)((const uint16_t *)a.x + (int64_t)m * K);
-  u32x4 xv[kSkPrepChunks];
+  __shared__ float red[4][8];
+  const int th = threadIdx.x, r = th & 7, wave = th >> 6;
+  const int m = 8 * (int)blockIdx.x + r;
+  const int K = a.K, nst = K / UK, nq = K / 8;
+  const int qb = (int)blockIdx.y * 32 * CH + (th >> 3);
+  const u32x4 *xr = (const u32x4 *)((const uint16_t *)a.x + (int64_t)min(m, a.M - 1) * K);
+  u32x4 xv[CH];
+  f32x4 g0[CH], g1[CH];
 #pragma unroll
-  for (int i = 0; i < kSkPrepChunks; ++i) {
-    const int q = th + 256 * i;
-    xv[i] = q < nq ? xr[q] : u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < CH; ++i) {
+    const int q = qb + 32 * i;
+    xv[i] = q < nq && m < a.M ? xr[q] : u32x4{0u, 0u, 0u, 0u};
+    g0[i] = g1[i] = f32x4{1.f, 1.f, 1.f, 1.f};
+    if constexpr (GAM) {
+      if (q < nq) {
+        g0[i] = ((const f32x4 *)a.gamma)[2 * q];
+        g1[i] = ((const f32x4 *)a.gamma)[2 * q + 1];
+      }
+    }
   }
   float ss = 0.f;
+  u32x4 *xf = (u32x4 *)a.xf;
 #pragma unroll
-  for (int i = 0; i < kSkPrepChunks; ++i)
+  for (int i = 0; i < CH; ++i) {
+    const int q = qb + 32 * i;
+    const float g[8] = {g0[i][0], g0[i][1], g0[i][2], g0[i][3],
+                        g1[i][0], g1[i][1], g1[i][2], g1[i][3]};
+    u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const f32x2 f = unpack2<CT>(xv[i][e]);
       ss += f[0] * f[0] + f[1] * f[1];
+      o[e] = pack2<CT>(f[0] * g[2 * e], f[1] * g[2 * e + 1]);
     }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  if ((th & 63) == 0) red[th >> 6] = ss;
-  __syncthreads();
-  const float rs =
-      a.norm ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps) : 1.0f;
-#pragma unroll
-  for (int i = 0; i < kSkPrepChunks; ++i) {
-    const int q = th + 256 * i;
-    if (q >= nq) break;
-    const u32x4 v = xv[i];
-    f32x4 g0 = f32x4{1.f, 1.f, 1.f, 1.f}, g1 = g0;
-    if constexpr (GAM) {
-      g0 = ((const f32x4 *)a.gamma)[2 * q];
-      g1 = ((const f32x4 *)a.gamma)[2 * q + 1];
+    if (q < nq) {
+      const int st = q / QPS, qq = q - st * QPS;
+      int j, gg;
+      sk_chunk_slot<FP8>(qq, j, gg);
+      xf[(((int64_t)(m >> 5) * nst + st) * KS + j) * 64 + 32 * gg + (m & 31)] = o;
     }
-    const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const f32x2 f = unpack2<CT>(v[e]);
-      o[e] = pack2<CT>(f[0] * rs * g[2 * e], f[1] * rs * g[2 * e + 1]);
-    }
-    out(q) = o;
   }
+  // row r: lanes r, r + 8, ... of each wave, then the four waves in order
+  ss += __shfl_xor(ss, 8, 64);
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  if ((th & 63) < 8) red[wave][r] = ss;
+  __syncthreads();
+  if (th < 8)
+    pss[blockIdx.y * 64 + 8 * blockIdx.x + th] =
+        ((red[0][th] + red[1][th]) + red[2][th]) + red[3][th];
 }
 
 // ---------------------------------------------------------------------------
@@ -217,7 +224,8 @@ sk_kernel(const SkArgs a) {
   constexpr int XST = MT * KS * 1024;      // XR: x B-operand bytes of one stage
   __shared__ __attribute__((aligned(1024))) unsigned char ldsx[XR ? 2 * XST : 16];
   __shared__ float s_sq[XR ? 64 : 1];     // XR: row sums of squares (this k-range)
-  __shared__ float s_rs[XR ? 64 : 1];     // XR: row scales
+  __shared__ float s_rs[64];              // row scales
+  __shared__ float s_pss[XR ? 1 : kSkPrepMaxSlices * 64];  // prep form: the prep's row sums
 
   const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
   const int N = a.N, K = a.K;
@@ -378,6 +386,16 @@ sk_kernel(const SkArgs a) {
   // hoisted ahead of its phase would wait for loads issued just before, and
   // the prologue keeps the loop's load order (the wait counts at the loop
   // head are the minimum over both ways in).
+  if constexpr (!XR) {
+    // the prep's per-slice row sums, 64 floats per copy (wave w: slices w,
+    // w + 4, ...), into LDS; read after the main loop's barriers
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.pss, (uint32_t)a.nsl * 256u);
+#pragma unroll
+    for (int i = 0; i < kSkPrepMaxSlices / 4; ++i) {
+      const int s = wave + 4 * i;
+      sk_lds_copy4(srs, (unsigned char *)(s_pss + 64 * s), s < a.nsl ? (uint32_t)(s * 64 + lane) * 4u : kOOB);
+    }
+  }
   static_for<0, NS - 1>([&](auto pc) {
     static_for<0, NV>([&](auto vc) { issue(vc, decltype(pc)::value, pc); });
     __builtin_amdgcn_sched_barrier(0);
@@ -452,7 +470,7 @@ sk_kernel(const SkArgs a) {
     const int m = 32 * ot + (lane & 31);
     if (m >= a.M) return;
     f32x16 r = r0;
-    if constexpr (XR) r *= s_rs[m];
+    r *= s_rs[m];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = n0 + 32 * ou + 8 * g + 4 * ag;
@@ -482,6 +500,15 @@ sk_kernel(const SkArgs a) {
   auto set_rs = [&](float ss) {
     if (th < 32 * MT) s_rs[th] = a.norm ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
   };
+  if constexpr (!XR) {
+    // the prep's slices in order (its copies landed before the main loop's
+    // first wait)
+    float ss = 0.f;
+    if (th < 32 * MT)
+      for (int s = 0; s < a.nsl; ++s) ss += s_pss[64 * s + th];
+    set_rs(ss);
+    __syncthreads();
+  }
   if (a.S == 1) {
     if constexpr (XR) {
       set_rs(ssw);

@@ -9,7 +9,8 @@ namespace mtp {
 
 constexpr int kSkBN = 64;   // output columns per workgroup
 constexpr int kSkUB = 128;  // W bytes per row per stage
-constexpr int kSkPrepChunks = 8;  // 16-byte chunks of a row of x per prep thread (K <= 16384)
+constexpr int kSkMaxK = 16384;    // K at most (the prep's slices cover 16 x 1024 k)
+constexpr int kSkPrepMaxSlices = 16;  // K-slices of the 8-row prep (row sums per slice)
 
 struct SkPrepArgs {
   const void *x;       // [M, K] in the compute type
@@ -35,15 +36,18 @@ struct SkArgs {
   int G, S, kb_per, nkb;  // column tiles, K-splits, stages per split, stages
   float *part;            // split-K partials
   unsigned *ticket;       // [G] arrival tickets (S > 1)
+  const float *pss;       // prep form: the prep's row sums of squares [nsl][64]
+  int nsl;                // prep form: the prep's K-slices
 };
 
 typedef void (*SkKernel)(SkArgs);
-typedef void (*SkPrepKernel)(SkPrepArgs);
+typedef void (*SkPrep8Kernel)(SkPrepArgs, float *);
+// 8-row prep for x dtype ct, the k-slot order of W dtype wt, gamma present,
+// 256 ch k per slice (ch 1, 2 or 4), or null.
+SkPrep8Kernel sk_prep8_pick(int ct, int wt, bool gam, int ch);
 // GEMM for x dtype ct (BF16 / F16), W dtype wt (FP8E4M3 or ct), mt 32-row
 // tiles of x (1 or 2), reading the prep's xn blocks or (xr) raw x, or null.
 SkKernel sk_pick(int ct, int wt, int mt, bool xr);
-// Prep for x dtype ct, the k-slot order of W dtype wt, gamma present, or null.
-SkPrepKernel sk_prep_pick(int ct, int wt, bool gam);
 
 // Bytes of the xn blocks for m rows of x and k columns.
 constexpr size_t sk_xf_bytes(int64_t m, int64_t k) {
