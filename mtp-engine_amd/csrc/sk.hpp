@@ -1,8 +1,9 @@
 // Skinny weight-streaming GEMM for gfx950: the RMSNorm -> linear path at
 // M <= 64 rows of x with 16-bit x (bf16 / f16) and fp8-e4m3 or 16-bit W.
 //
-//   y[m, n] = (xn[m, :] . W[n, :]) * wscale[n] + bias[n], times scale
-//   xn[m, k] = x[m, k] * rs[m] * gamma[k],  rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) (norm) or 1
+//   y[m, n] = (rs[m] (xg[m, :] . W[n, :]) * wscale[n] + bias[n]), times scale
+//   xg[m, k] = x[m, k] * gamma[k] rounded to the type of x,
+//   rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) (norm) or 1 (applied to the fp32 sums)
 //
 // Two launches (one without gamma: the raw-x form below):
 //  1. sk_prep8_kernel, blocks of 8 rows x one K-slice (rows padded to whole
@@ -36,7 +37,7 @@
 //     k-slot order: within 32 k of a stage (two k-steps for fp8), lane group
 //     g = lane / 32 holds k 16 g .. 16 g + 15, the first 8 in k-step 2p, the
 //     other 8 in k-step 2p + 1 (16-bit W: k-step j, lane group g holds
-//     k 16 j + 8 g .. + 7); the prep writes xn in the same order.
+//     k 16 j + 8 g .. + 7); the prep writes xg in the same order.
 //  The stages of a split are taken starting at 7 tile mod (stages): tiles in
 //  step with each other then read different 128-byte offsets of their rows,
 //  which spreads the requests over the HBM channels (the same offset of every
