@@ -23,10 +23,10 @@
 //     copies W (64 rows x 128 bytes: one instruction covers 8 rows x 128
 //     contiguous bytes, the pattern that streams HBM fastest among the ones
 //     an MFMA row layout allows) into registers, and each wave loads its own
-//     xn blocks (1 KB contiguous per MFMA operand) into registers. W bytes in
-//     flight per CU set the bandwidth (register loads keep more of them in
-//     flight per CU than buffer loads into LDS), so both register rings run
-//     NS - 1 stages ahead (NS = 8: 56 KB of W per CU); the loads of a stage
+//     xn blocks (1 KB contiguous per MFMA operand) into registers. Both
+//     register rings run NS - 1 stages ahead (NS = 6: 40 KB of W per CU;
+//     register loads keep more bytes in flight per CU than buffer loads into
+//     LDS, and a deeper ring measured slower); the loads of a stage
 //     are spread over the wave's MFMAs. One stage before it is used, a stage
 //     of W goes from registers to LDS (double-buffered), where each wave
 //     reads the A operands of its k-steps. One barrier per stage.
@@ -214,7 +214,12 @@ sk_kernel(const SkArgs a) {
   constexpr int KS = UK / 16;                // MFMA k-steps per stage
   constexpr int KPW = KS / 4;                // k-steps per wave per stage
   constexpr int STAGE = kSkBN * kSkUB;       // W bytes of one LDS buffer (8 KB)
-  constexpr int NS = 8;                      // register ring stages (loads run NS - 1 ahead)
+  // register ring stages (loads run NS - 1 ahead; even: LDS buffer = slot
+  // parity). 6 measured faster than 8 on every shape tried (fp8 64 x 14336
+  // x 4096 23.1 against 23.9 us; bf16 64 x 4096 x 4096 without gamma 13.4
+  // against 14.1); 4 only ties it at fp8 with gamma and 64 rows and loses
+  // elsewhere (bf16 64 x 4096 x 4096 14.6, fp8 32 x 14336 x 4096 20.5)
+  constexpr int NS = 6;
   constexpr int NWC = STAGE / 1024 / 4;      // W loads per wave per stage (2)
   constexpr int NXL = MT * KPW;              // xn loads per wave per stage
   constexpr int NV = NWC + NXL;              // vector-memory instructions per wave per stage
