@@ -18,9 +18,10 @@ struct Sf32Args {
   float eps, scale;
 };
 
-constexpr int kSf32MaxK = 1024;  // k per launch: kSf32Waves waves x 16 floats per load
-// waves per workgroup, each KPW = kSf32MaxK / kSf32Waves k (4, 8 and 16
-// measured alike at M 16, K 1024, N 4096: 7.4, 7.4, 7.6 us per call)
+constexpr int kSf32MaxK = 1024;  // k per launch: kSf32Waves waves x KPW k, all staged in LDS
+// waves per workgroup, each KPW = kSf32MaxK / kSf32Waves k (4 and 8
+// measured 6.7 and 6.9 us per call at M 16, K 1024, N 4096; 16 waves' LDS
+// areas and sums do not fit the 160 KB)
 constexpr int kSf32Waves = 4;
 
 // Launch for fp32 x and W, 1 <= M <= 16, 16 <= K <= kSf32MaxK with
