@@ -349,13 +349,13 @@ def test_single_launch_default_route_few_rows(M, N, K, wkind):
 
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (1, 5, 16), (3, 17, 1008), (16, 130, 512),
                                    (9, 64, 272), (12, 1000, 48)])
-@pytest.mark.parametrize("bias_dt", [None, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("bias_dt", [None, torch.float32, torch.bfloat16, torch.float16])
 def test_small_fp32_kernel(M, N, K, bias_dt):
     """fp32 x and W with at most 16 rows and K <= 1024 take the one-launch
     fp32 kernel by default (every load of the launch in one round trip):
     ragged N (scalar stores), K not a multiple of the 256-k wave range,
-    gamma / norm / bias / scale on and off, rtol 1e-5 against the oracle;
-    tuning key sf32=0 gives the tiled kernel the same answer."""
+    gamma / norm / bias (fp32, bf16, f16) / scale on and off, rtol 1e-5
+    against the oracle; tuning key sf32=0 gives the tiled kernel the same answer."""
     from mtp_hip import ops
     print(f"case sf32 M={M} N={N} K={K} bias={bias_dt}", flush=True)
     g = torch.Generator().manual_seed(M * 7 + N + K)
