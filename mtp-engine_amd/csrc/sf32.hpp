@@ -187,4 +187,165 @@ __global__ void __launch_bounds__(64 * NW, 1) sf32_kernel(const Sf32Args a) {
   }
 }
 
+// 4 bytes per lane from a buffer straight into LDS (lane i writes bytes
+// 4 i .. 4 i + 3 after `lds`); device pass only.
+__device__ __forceinline__ void sf32_dma4(__amdgpu_buffer_rsrc_t r, unsigned char *lds,
+                                          uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4,
+                                           voff, 0, 0, 0);
+#else
+  (void)r; (void)lds; (void)voff;
+#endif
+}
+
+// Streaming form for K > kSf32MaxK (the same 16-column workgroups, the same
+// sums): wave w owns k = KW w .. KW w + KW - 1 (KW = K / NW rounded up to 64)
+// and streams it in blocks of 64 k through a ring of kSf32Ring blocks in its
+// own LDS area. A block's copies: gamma (4 bytes per lane, 64 k), then x,
+// then W, each 4 rows x 256 contiguous bytes per instruction with the
+// chunk c of row r at slot c ^ r, as above. Block b is waited for with a
+// fixed count (the kSf32Ring - 1 younger blocks in flight), its 16 MFMAs
+// run, and its slot is refilled with block b + kSf32Ring; refills past the
+// wave's range use out-of-range offsets (zeros, no memory access) so the
+// count stays fixed.
+template <bool GAM, int NW>
+__global__ void __launch_bounds__(64 * NW, 1) sf32s_kernel(const Sf32Args a) {
+  constexpr int RD = kSf32Ring;
+  constexpr int WB = 4096;                       // one 64-k block of 16 rows
+  constexpr int SLOT = 2 * WB + (GAM ? 256 : 0);  // W, x, gamma
+  constexpr int C = 8 + (GAM ? 1 : 0);            // copy instructions per block
+  static_assert((RD - 1) * C < 64, "vmcnt is 6 bits");
+  constexpr int LD = NW * RD * SLOT;
+  // one LDS object (see sf32_kernel): the rings, then the waves' sums
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LD + NW * (64 * 16 + 16 * 4)];
+  f32x4(*const s_acc)[64] = (f32x4(*)[64])(lds + LD);
+  float(*const s_ss)[16] = (float(*)[16])(lds + LD + NW * 64 * 16);
+  const int th = threadIdx.x, lane = th & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const int K = a.K;
+  const int KW = (K + 64 * NW - 1) / (64 * NW) * 64;  // k per wave
+  const int nb = KW / 64;                             // blocks per wave
+  const int kw0 = KW * wave;
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(a.w + (int64_t)n0 * K, (uint32_t)(min(16, a.N - n0) * K) * 4u);
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)(a.M * K) * 4u);
+  const __amdgpu_buffer_rsrc_t grs = make_rsrc(a.gamma, GAM ? (uint32_t)K * 4u : 0u);
+  // raw bias of the lane's output columns n0 + 4 g + e, before the ring
+  uint32_t braw[4] = {0u, 0u, 0u, 0u};
+  if (a.bias) {
+    const uint32_t nbias = (uint32_t)(n0 + 4 * g);
+    if (a.bias_dt == MTP_F32) {
+      const __amdgpu_buffer_rsrc_t brs = make_rsrc(a.bias, (uint32_t)a.N * 4u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        braw[e] = __builtin_amdgcn_raw_buffer_load_b32(brs, (nbias + e) * 4u, 0, 0);
+    } else {
+      const __amdgpu_buffer_rsrc_t brs = make_rsrc(a.bias, (uint32_t)a.N * 2u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        braw[e] = __builtin_amdgcn_raw_buffer_load_b16(brs, (nbias + e) * 2u, 0, 0);
+    }
+  }
+  unsigned char *const ring = lds + wave * RD * SLOT;
+  // copy q of a block: row rr = 4 q + lane / 16, chunk (lane % 16) ^ rr
+  int rq[4], kq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    rq[q] = 4 * q + (lane >> 4);
+    kq[q] = 4 * ((lane & 15) ^ rq[q]);
+  }
+  auto issue = [&](int blk, auto slotc) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slotc)::value;
+    unsigned char *const sb = ring + slot * SLOT;
+    const int kb = kw0 + 64 * blk;
+    const bool live = blk < nb;
+    if constexpr (GAM)
+      sf32_dma4(grs, sb + 2 * WB, live && kb + lane < K ? (uint32_t)(kb + lane) * 4u : kOOB);
+    uint32_t off[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int k = kb + kq[q];
+      off[q] = live && k < K ? (uint32_t)(rq[q] * K + k) * 4u : kOOB;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sf32_dma16(xrs, sb + WB + 1024 * q, off[q], 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sf32_dma16(wrs, sb + 1024 * q, off[q], 1);
+  };
+  static_for<0, RD>([&](auto sc) { issue(decltype(sc)::value, sc); });
+
+  float ss = 0.f;
+  f32x4 ac[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ac[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int b0 = 0; b0 < nb; b0 += RD) {
+    static_for<0, RD>([&](auto sc) {
+      constexpr int slot = decltype(sc)::value;
+      const int blk = b0 + slot;
+      if (blk < nb) {
+        // block blk's copies have landed (the RD - 1 younger blocks may not)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((RD - 1) * C) : "memory");
+        const unsigned char *const sb = ring + slot * SLOT;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int off = 256 * r + 16 * ((4 * jj + g) ^ r);
+          const f32x4 wv = *(const f32x4 *)(sb + off);
+          const f32x4 xv = *(const f32x4 *)(sb + WB + off);
+          f32x4 gv = f32x4{1.f, 1.f, 1.f, 1.f};
+          if constexpr (GAM) gv = *(const f32x4 *)(sb + 2 * WB + 64 * jj + 16 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float xe = xv[e];
+            ss = __builtin_fmaf(xe, xe, ss);
+            const float bx = GAM ? xe * gv[e] : xe;
+            ac[e] = mfma16_f32(wv[e], bx, ac[e]);
+          }
+        }
+        // the slot's reads are done before its refill is issued
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(blk + RD, sc);
+      }
+    });
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // refills past the end
+  const f32x4 acc = ((ac[0] + ac[1]) + ac[2]) + ac[3];
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  if (g == 0) s_ss[wave][r] = ss;
+  s_acc[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 t = s_acc[0][lane];
+  float sq = s_ss[0][r];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    t += s_acc[w][lane];
+    sq += s_ss[w][r];
+  }
+  const float rs = a.norm ? 1.0f / sqrtf(sq / (float)K + a.eps) : 1.0f;
+  const int m = r;
+  if (m >= a.M) return;
+  const int n = n0 + 4 * g;
+  float o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float bi = !a.bias                  ? 0.f
+                     : a.bias_dt == MTP_F32   ? __builtin_bit_cast(float, braw[e])
+                     : a.bias_dt == MTP_BF16 ? bf16_bits_to_f32(braw[e])
+                                              : f16_bits_to_f32(braw[e]);
+    o[e] = (a.bias ? t[e] * rs + bi : t[e] * rs) * a.scale;
+  }
+  float *yr = a.y + (int64_t)m * a.N;
+  if (n + 3 < a.N && (a.N & 3) == 0) {
+    *(f32x4 *)(yr + n) = f32x4{o[0], o[1], o[2], o[3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < a.N) yr[n + e] = o[e];
+  }
+}
+
 }  // namespace mtp

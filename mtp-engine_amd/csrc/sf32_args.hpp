@@ -24,7 +24,13 @@ constexpr int kSf32MaxK = 1024;  // k per launch: kSf32Waves waves x KPW k, all 
 // areas and sums do not fit the 160 KB)
 constexpr int kSf32Waves = 4;
 
-// Launch for fp32 x and W, 1 <= M <= 16, 16 <= K <= kSf32MaxK with
+// Streaming form (sf32s_kernel) for kSf32MaxK < K <= kSf32StreamMaxK: each
+// wave streams its K-range in 64-k blocks through an LDS ring of
+// kSf32Ring blocks (8 KB of x and W each, 32 KB per wave in flight).
+constexpr int kSf32StreamMaxK = 65536;
+constexpr int kSf32Ring = 4;
+
+// Launch for fp32 x and W, 1 <= M <= 16, 16 <= K <= kSf32StreamMaxK with
 // K % 16 == 0, 16-byte aligned x / W / gamma / y (MTP_ERR_SHAPE otherwise).
 int launch_sf32(const Sf32Args &a, hipStream_t st);
 
