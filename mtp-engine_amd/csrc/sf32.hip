@@ -11,11 +11,11 @@ int launch_sf32(const Sf32Args &a, hipStream_t st) {
   const unsigned blocks = (unsigned)((a.N + 15) / 16);
   if (a.K > kSf32MaxK) {
     if (a.gamma)
-      hipLaunchKernelGGL((sf32s_kernel<true, kSf32Waves>), dim3(blocks), dim3(64 * kSf32Waves), 0,
-                         st, a);
+      hipLaunchKernelGGL((sf32s_kernel<true, kSf32sWaves>), dim3(blocks), dim3(64 * kSf32sWaves),
+                         0, st, a);
     else
-      hipLaunchKernelGGL((sf32s_kernel<false, kSf32Waves>), dim3(blocks), dim3(64 * kSf32Waves), 0,
-                         st, a);
+      hipLaunchKernelGGL((sf32s_kernel<false, kSf32sWaves>), dim3(blocks), dim3(64 * kSf32sWaves),
+                         0, st, a);
     return launch_status();
   }
   if (a.gamma)

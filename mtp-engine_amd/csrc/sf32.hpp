@@ -202,7 +202,8 @@ __device__ __forceinline__ void sf32_dma4(__amdgpu_buffer_rsrc_t r, unsigned cha
 // Streaming form for K > kSf32MaxK (the same 16-column workgroups, the same
 // sums): wave w owns k = KW w .. KW w + KW - 1 (KW = K / NW rounded up to 64)
 // and streams it in blocks of 64 k through a ring of kSf32Ring blocks in its
-// own LDS area. A block's copies: gamma (4 bytes per lane, 64 k), then x,
+// own LDS area (with one block per wave, the other waves of its SIMD keep
+// the memory busy while it waits). A block's copies: gamma (4 bytes per lane, 64 k), then x,
 // then W, each 4 rows x 256 contiguous bytes per instruction with the
 // chunk c of row r at slot c ^ r, as above. Block b is waited for with a
 // fixed count (the kSf32Ring - 1 younger blocks in flight), its 16 MFMAs

@@ -25,10 +25,15 @@ constexpr int kSf32MaxK = 1024;  // k per launch: kSf32Waves waves x KPW k, all 
 constexpr int kSf32Waves = 4;
 
 // Streaming form (sf32s_kernel) for kSf32MaxK < K <= kSf32StreamMaxK: each
-// wave streams its K-range in 64-k blocks through an LDS ring of
-// kSf32Ring blocks (8 KB of x and W each, 32 KB per wave in flight).
+// of kSf32sWaves waves streams its K-range in 64-k blocks (4 KB of W, 4 KB
+// of x) through an LDS ring of kSf32Ring blocks. Fewer bytes in flight per
+// wave and more waves measured faster (us per call, 8 waves x 1 block /
+// 8 x 2 / 4 x 4: fp32 8 x 4096 x 4096 14.0 / 14.0 / 16.0, 8 x 14336 x 4096
+// 42.8 / 48.0 / 53.9, 16 x 4096 x 2048 8.9 / 9.5 / 9.7; 16 waves x 1 block
+// 16.2 at 8 x 4096 x 4096; a deeper W ring than x ring was slower still).
 constexpr int kSf32StreamMaxK = 65536;
-constexpr int kSf32Ring = 4;
+constexpr int kSf32Ring = 1;
+constexpr int kSf32sWaves = 8;
 
 // Launch for fp32 x and W, 1 <= M <= 16, 16 <= K <= kSf32StreamMaxK with
 // K % 16 == 0, 16-byte aligned x / W / gamma / y (MTP_ERR_SHAPE otherwise).
