@@ -1,6 +1,6 @@
 """HIP-graph capture of the hot path: a draft step (RMSNorm, RMSNorm ->
-linear head, greedy token + embedding, combine-norm), the fp32 row-chunk
-linear with K-splits, the persistent multi-verify and the device-side
+linear head, greedy token + embedding, combine-norm), the fp32 linear
+routes (one launch, streaming, row-chunk with K-splits), the persistent multi-verify and the device-side
 commit are each captured once on a warmed-up stream and replayed with new
 input contents; every replay equals the eager result bit for bit (the
 kernels re-arm their tickets and keys themselves), with eager work and
@@ -64,19 +64,30 @@ def test_draft_step_graph_replay():
     _replays(graph, out, lambda i: hidden.copy_(seeds[i]), step)
 
 
-def test_fp32_row_chunk_linear_graph_replay():
-    """The fp32 TF32-off route (row-chunk kernel with grid K-splits) under
-    capture: the split-K tickets are re-armed on every replay."""
-    from mtp_hip import ops, workloads
-    d = workloads.fp32_linear()
+@pytest.mark.parametrize("route", ["small", "stream", "tiled"])
+def test_fp32_linear_graph_replay(route):
+    """The fp32 TF32-off routes under capture: the one-launch kernel (x [16,
+    1024]), the streaming kernel at the fp32 head's shape (x [8, 4096], W
+    [4096, 4096]) and the tiled row-chunk kernel with grid K-splits (tuning
+    key sf32 = 0; its split-K tickets are re-armed on every replay)."""
+    from mtp_hip import _lib as L, ops, workloads
+    if route == "stream":
+        d = workloads.fp32_linear(M=8, K=4096, N=4096)
+    else:
+        d = workloads.fp32_linear()
+    print(f"case fp32 graph route={route} x={tuple(d['x'].shape)}", flush=True)
     x = d["x"].to(DEV)
     W = d["weight"].to(DEV)
     gm = d["gamma"].to(DEV)
-    fn = lambda: ops.rmsnorm_linear(x, W, None, d["eps"], 1.0, gamma=gm)  # noqa: E731
-    graph, out = _capture(fn)
-    g = torch.Generator().manual_seed(2)
-    xs = [torch.randn(x.shape, generator=g).to(DEV) for _ in range(4)]
-    _replays(graph, out, lambda i: x.copy_(xs[i]), fn)
+    L.set_tuning(sf32=0 if route == "tiled" else -1)
+    try:
+        fn = lambda: ops.rmsnorm_linear(x, W, None, d["eps"], 1.0, gamma=gm)  # noqa: E731
+        graph, out = _capture(fn)
+        g = torch.Generator().manual_seed(2)
+        xs = [torch.randn(x.shape, generator=g).to(DEV) for _ in range(4)]
+        _replays(graph, out, lambda i: x.copy_(xs[i]), fn)
+    finally:
+        L.set_tuning(sf32=-1)
 
 
 def test_multi_verify_graph_replay():
