@@ -210,18 +210,19 @@ __device__ __forceinline__ void sf32_dma4(__amdgpu_buffer_rsrc_t r, unsigned cha
 // run, and its slot is refilled with block b + kSf32Ring; refills past the
 // wave's range use out-of-range offsets (zeros, no memory access) so the
 // count stays fixed.
-template <bool GAM, int NW>
+template <bool GAM, int NW, int MT>
 __global__ void __launch_bounds__(64 * NW, 1) sf32s_kernel(const Sf32Args a) {
   constexpr int RD = kSf32Ring;
   constexpr int WB = 4096;                       // one 64-k block of 16 rows
-  constexpr int SLOT = 2 * WB + (GAM ? 256 : 0);  // W, x, gamma
-  constexpr int C = 8 + (GAM ? 1 : 0);            // copy instructions per block
+  constexpr int GO = (1 + MT) * WB;                // gamma's offset in a slot
+  constexpr int SLOT = GO + (GAM ? 256 : 0);        // W, MT x tiles, gamma
+  constexpr int C = 4 + 4 * MT + (GAM ? 1 : 0);     // copy instructions per block
   static_assert((RD - 1) * C < 64, "vmcnt is 6 bits");
   constexpr int LD = NW * RD * SLOT;
   // one LDS object (see sf32_kernel): the rings, then the waves' sums
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[LD + NW * (64 * 16 + 16 * 4)];
-  f32x4(*const s_acc)[64] = (f32x4(*)[64])(lds + LD);
-  float(*const s_ss)[16] = (float(*)[16])(lds + LD + NW * 64 * 16);
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LD + NW * MT * (64 * 16 + 16 * 4)];
+  f32x4(*const s_acc)[MT][64] = (f32x4(*)[MT][64])(lds + LD);
+  float(*const s_ss)[MT][16] = (float(*)[MT][16])(lds + LD + NW * MT * 64 * 16);
   const int th = threadIdx.x, lane = th & 63;
   const int wave = __builtin_amdgcn_readfirstlane(th >> 6);
   const int g = lane >> 4, r = lane & 15;
@@ -264,24 +265,33 @@ __global__ void __launch_bounds__(64 * NW, 1) sf32s_kernel(const Sf32Args a) {
     const int kb = kw0 + 64 * blk;
     const bool live = blk < nb;
     if constexpr (GAM)
-      sf32_dma4(grs, sb + 2 * WB, live && kb + lane < K ? (uint32_t)(kb + lane) * 4u : kOOB);
+      sf32_dma4(grs, sb + GO, live && kb + lane < K ? (uint32_t)(kb + lane) * 4u : kOOB);
     uint32_t off[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int k = kb + kq[q];
       off[q] = live && k < K ? (uint32_t)(rq[q] * K + k) * 4u : kOOB;
     }
+    // x tile t: rows 16 t + rr (rows past M read 0 through the range)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sf32_dma16(xrs, sb + WB + 1024 * q, off[q], 0);
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        sf32_dma16(xrs, sb + (1 + t) * WB + 1024 * q,
+                   off[q] == kOOB ? kOOB : off[q] + (uint32_t)(64 * t * K), 0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) sf32_dma16(wrs, sb + 1024 * q, off[q], 1);
   };
   static_for<0, RD>([&](auto sc) { issue(decltype(sc)::value, sc); });
 
-  float ss = 0.f;
-  f32x4 ac[4];
+  float ss[MT];
+  f32x4 ac[MT][4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) ac[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < MT; ++t) {
+    ss[t] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ac[t][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   for (int b0 = 0; b0 < nb; b0 += RD) {
     static_for<0, RD>([&](auto sc) {
       constexpr int slot = decltype(sc)::value;
@@ -294,16 +304,20 @@ __global__ void __launch_bounds__(64 * NW, 1) sf32s_kernel(const Sf32Args a) {
         for (int jj = 0; jj < 4; ++jj) {
           const int off = 256 * r + 16 * ((4 * jj + g) ^ r);
           const f32x4 wv = *(const f32x4 *)(sb + off);
-          const f32x4 xv = *(const f32x4 *)(sb + WB + off);
-          f32x4 gv = f32x4{1.f, 1.f, 1.f, 1.f};
-          if constexpr (GAM) gv = *(const f32x4 *)(sb + 2 * WB + 64 * jj + 16 * g);
+          f32x4 xv[MT];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float xe = xv[e];
-            ss = __builtin_fmaf(xe, xe, ss);
-            const float bx = GAM ? xe * gv[e] : xe;
-            ac[e] = mfma16_f32(wv[e], bx, ac[e]);
-          }
+          for (int t = 0; t < MT; ++t) xv[t] = *(const f32x4 *)(sb + (1 + t) * WB + off);
+          f32x4 gv = f32x4{1.f, 1.f, 1.f, 1.f};
+          if constexpr (GAM) gv = *(const f32x4 *)(sb + GO + 64 * jj + 16 * g);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float xe = xv[t][e];
+              ss[t] = __builtin_fmaf(xe, xe, ss[t]);
+              const float bx = GAM ? xe * gv[e] : xe;
+              ac[t][e] = mfma16_f32(wv[e], bx, ac[t][e]);
+            }
         }
         // the slot's reads are done before its refill is issued
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -312,22 +326,27 @@ __global__ void __launch_bounds__(64 * NW, 1) sf32s_kernel(const Sf32Args a) {
     });
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // refills past the end
-  const f32x4 acc = ((ac[0] + ac[1]) + ac[2]) + ac[3];
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
-  if (g == 0) s_ss[wave][r] = ss;
-  s_acc[wave][lane] = acc;
+#pragma unroll
+  for (int tt = 0; tt < MT; ++tt) {
+    float v = ss[tt];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (g == 0) s_ss[wave][tt][r] = v;
+    s_acc[wave][tt][lane] = ((ac[tt][0] + ac[tt][1]) + ac[tt][2]) + ac[tt][3];
+  }
   __syncthreads();
-  if (wave != 0) return;
-  f32x4 t = s_acc[0][lane];
-  float sq = s_ss[0][r];
+  // wave tt < MT finishes row tile tt, the waves' sums in wave order
+  if (wave >= MT) return;
+  const int tt = wave;
+  f32x4 t = s_acc[0][tt][lane];
+  float sq = s_ss[0][tt][r];
 #pragma unroll
   for (int w = 1; w < NW; ++w) {
-    t += s_acc[w][lane];
-    sq += s_ss[w][r];
+    t += s_acc[w][tt][lane];
+    sq += s_ss[w][tt][r];
   }
   const float rs = a.norm ? 1.0f / sqrtf(sq / (float)K + a.eps) : 1.0f;
-  const int m = r;
+  const int m = 16 * tt + r;
   if (m >= a.M) return;
   const int n = n0 + 4 * g;
   float o[4];

@@ -35,7 +35,8 @@ constexpr int kSf32StreamMaxK = 65536;
 constexpr int kSf32Ring = 1;
 constexpr int kSf32sWaves = 8;
 
-// Launch for fp32 x and W, 1 <= M <= 16, 16 <= K <= kSf32StreamMaxK with
+// Launch for fp32 x and W, 1 <= M <= 32 (more than 16 rows or K past
+// kSf32MaxK: the streaming form), 16 <= K <= kSf32StreamMaxK with
 // K % 16 == 0, 16-byte aligned x / W / gamma / y (MTP_ERR_SHAPE otherwise).
 int launch_sf32(const Sf32Args &a, hipStream_t st);
 
