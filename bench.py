@@ -105,9 +105,11 @@ def make_fp8_case(torch, lib, L, M: int):
     return case
 
 
-def make_fp32_case(torch, lib, L):
+def make_fp32_case(torch, lib, L, M=16, K=1024, N=4096):
+    """fp32 RMSNorm+linear (TF32 off); the default is the fp32 configuration,
+    M=8, K=4096 the MTP head's shape (opt-in with --only fp32_M8_K4096)."""
     from mtp_hip import workloads
-    d = workloads.fp32_linear()
+    d = workloads.fp32_linear(M=M, K=K, N=N)
     dev = torch.device("cuda")
     M, K = d["x"].shape
     N = d["weight"].shape[0]
@@ -129,7 +131,7 @@ def make_fp32_case(torch, lib, L):
             raise RuntimeError(f"fp32 launch failed: {st}")
 
     nbytes = M * K * 4 + N * K * 4 + K * 4 + M * N * 4
-    case = Case("fp32_rmsnorm_linear_M16", launch, nbytes, 2 * M * N * K, "hbm", nrot)
+    case = Case(f"fp32_rmsnorm_linear_M{M}_K{K}_N{N}", launch, nbytes, 2 * M * N * K, "hbm", nrot)
     case.keep = (wl, x, gamma, y, ws)
     return case
 
@@ -365,6 +367,8 @@ def main():
                 ("int4_M256", lambda: make_int4_case(torch, lib, L))]
     if args.only:
         builders = [b for b in builders if b[0] in args.only.split(",")]
+        if "fp32_M8_K4096" in args.only.split(","):  # opt-in: the MTP head's fp32 shape
+            builders.append(("fp32_M8_K4096", lambda: make_fp32_case(torch, lib, L, 8, 4096)))
     for key, mk in builders:
         log(f"[bench] building {key}")
         case = mk()
@@ -374,7 +378,7 @@ def main():
         gbs = case.nbytes / (ms * 1e-3) / 1e9
         tfl = case.flops / (ms * 1e-3) / 1e12
         hbm_frac = gbs / HBM_PEAK_GBS
-        mfma_frac = tfl / (FP32_MFMA_PEAK_TFLOPS if key == "fp32_M16" else BF16_MFMA_PEAK_TFLOPS)
+        mfma_frac = tfl / (FP32_MFMA_PEAK_TFLOPS if key.startswith("fp32") else BF16_MFMA_PEAK_TFLOPS)
         detail[key] = dict(workload=case.name, us_per_call=round(us, 3), GBps=round(gbs, 1),
                            TFLOPs=round(tfl, 2), bound=case.bound,
                            roofline_frac=round(hbm_frac if case.bound == "hbm" else mfma_frac, 4),
