@@ -83,7 +83,7 @@ const char *mtp_last_hip_error(void);
  * "verify_wstream" (1 = column-group verify kernel), "skp" (1 force / 0
  * disable the x-resident skinny kernel), "skp_splits", "skp_ta" (A tiles
  * per wave: 1, 2 or 4), "skp_h8" (0: full x blocks in the x-resident
- * kernel for at most 8 rows), "sf32" (0: no small fp32 kernel), "attn32"
+ * kernel for at most 8 rows), "sf32" (0: no one-launch fp32 kernels for at most 32 rows), "attn32"
  * (0: 16-query-tile attention for 33 .. 64 queries), "sk_xraw" (0: the
  * skinny kernel keeps its prep launch without gamma too). value -1 restores the
  * planner's choice. The MTP_SKL, MTP_SK_SPLITS, MTP_WS_TUNE
