@@ -1,5 +1,7 @@
-// Small fp32 RMSNorm -> linear for gfx950 (TF32 off): at most 16 rows of
-// fp32 x, fp32 W, K <= 1024, one launch, one round trip of loads.
+// Small fp32 RMSNorm -> linear for gfx950 (TF32 off), one launch of
+// 16-column workgroups: sf32_kernel for at most 16 rows of fp32 x and
+// K <= 1024 (one round trip of loads), sf32s_kernel (below) for larger K or
+// 17 .. 32 rows (each wave's K-range streamed through LDS).
 //
 //   y[m, n] = (rs[m] * sum_k (x[m, k] gamma[k]) W[n, k] + bias[n]) * scale,
 //   rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) (norm) or 1
@@ -199,17 +201,19 @@ __device__ __forceinline__ void sf32_dma4(__amdgpu_buffer_rsrc_t r, unsigned cha
 #endif
 }
 
-// Streaming form for K > kSf32MaxK (the same 16-column workgroups, the same
-// sums): wave w owns k = KW w .. KW w + KW - 1 (KW = K / NW rounded up to 64)
-// and streams it in blocks of 64 k through a ring of kSf32Ring blocks in its
-// own LDS area (with one block per wave, the other waves of its SIMD keep
-// the memory busy while it waits). A block's copies: gamma (4 bytes per lane, 64 k), then x,
-// then W, each 4 rows x 256 contiguous bytes per instruction with the
-// chunk c of row r at slot c ^ r, as above. Block b is waited for with a
-// fixed count (the kSf32Ring - 1 younger blocks in flight), its 16 MFMAs
-// run, and its slot is refilled with block b + kSf32Ring; refills past the
-// wave's range use out-of-range offsets (zeros, no memory access) so the
-// count stays fixed.
+// Streaming form for K > kSf32MaxK or 17 .. 32 rows (the same 16-column
+// workgroups, the same sums; MT = 1 or 2 tiles of 16 x rows): wave w owns
+// k = KW w .. KW w + KW - 1 (KW = K / NW rounded up to 64) and streams it in
+// blocks of 64 k through a ring of kSf32Ring blocks in its own LDS area
+// (with one block per wave, the other waves of its SIMD keep the memory
+// busy while it waits). A block's copies: gamma (4 bytes per lane, 64 k),
+// then the MT x tiles, then W, each 4 rows x 256 contiguous bytes per
+// instruction with the chunk c of row r at slot c ^ r, as above. Block b is
+// waited for with a fixed count (the kSf32Ring - 1 younger blocks in
+// flight), its 16 MT MFMAs run (one W fragment feeds every tile), and its
+// slot is refilled with block b + kSf32Ring; refills past the wave's range
+// use out-of-range offsets (zeros, no memory access) so the count stays
+// fixed. Wave t < MT finishes row tile t.
 template <bool GAM, int NW, int MT>
 __global__ void __launch_bounds__(64 * NW, 1) sf32s_kernel(const Sf32Args a) {
   constexpr int RD = kSf32Ring;
