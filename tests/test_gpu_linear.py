@@ -350,12 +350,14 @@ def test_single_launch_default_route_few_rows(M, N, K, wkind):
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (1, 5, 16), (3, 17, 1008), (16, 130, 512),
                                    (9, 64, 272), (12, 1000, 48), (16, 4096, 4096), (7, 130, 1040),
                                    (16, 200, 8192), (1, 17, 2064), (17, 130, 1024),
-                                   (32, 4096, 4096), (24, 200, 1040), (32, 64, 48)])
+                                   (32, 4096, 4096), (24, 200, 1040), (32, 64, 48),
+                                   (8, 8192, 1024)])
 @pytest.mark.parametrize("bias_dt", [None, torch.float32, torch.bfloat16, torch.float16])
 def test_small_fp32_kernel(M, N, K, bias_dt):
     """fp32 x and W with at most 32 rows take the one-launch fp32 kernels by
-    default (at most 16 rows and K <= 1024: every load of the launch in one
-    round trip; otherwise each wave's K-range streamed through LDS, one or two
+    default (at most 16 rows, 512 < K <= 1024 and at most one workgroup per
+    CU: every load of the launch in one round trip, here at N 4096 and 17;
+    otherwise each wave's K-range streamed through LDS, one or two
     16-row tiles, ragged last blocks at K 1040 and 2064): ragged N (scalar stores), K not
     a multiple of the 256-k wave range,
     gamma / norm / bias (fp32, bf16, f16) / scale on and off, rtol 1e-5
