@@ -751,9 +751,10 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   a.eps = eps;
   a.scale = scale;
   a.norm = norm;
-  // fp32 x and W, <= 32 rows: one launch of 16-column workgroups; <= 16 rows
-  // and K <= 1024 every load in one round trip (fp32 K 1024 N 4096 16 rows:
-  // the planner's tiled kernel 9.9 us), otherwise streamed through LDS
+  // fp32 x and W, <= 32 rows: one launch of 16-column workgroups, every load
+  // in one round trip or each wave's K-range streamed through LDS
+  // (launch_sf32 picks; fp32 K 1024 N 4096 16 rows: the planner's tiled
+  // kernel 9.9 us)
   if (xt == MTP_F32 && wt == MTP_F32 && !wscale && tune(kTuneSf32) != 0 && M <= 32 &&
       K >= 16 && K <= kSf32StreamMaxK && K % 16 == 0 && aligned && (!gamma || gt == MTP_F32) &&
       tune(kTuneWsVariant) < 0 && tune(kTuneWsSplits) <= 0) {
