@@ -9,10 +9,10 @@ one call; weights rotate over enough copies that no call reads W from the
 256 MB Infinity Cache. Calls go straight through the C ABI with
 preallocated outputs on torch's current stream, timed with HIP events on
 that stream. Every other workload is timed in the same run into "detail"
-(fp8 at M = 8 / 32, the fp32 TF32-off linear, the multi-verify chain, the
+(fp8 at M = 8 / 32, the fp32 TF32-off linear, the multi-verify chain
+without and with the lm_head bias and in fp32 with the bias, the
 tree-verify step, the INT4 linear at M = 256), each with its roofline
-fraction against its own bound; "verify_step_us" holds the two verify
-steps.
+fraction against its own bound; "verify_step_us" holds the verify steps.
 
 Prints ONE JSON line. The CPU baselines time the oracle's eager
 restatement of the headline workload and of the fp32 configuration on this
@@ -50,11 +50,13 @@ def rotations(weight_bytes: int) -> int:
 
 class Case:
     """A workload bound to preallocated device buffers; launch(i) enqueues
-    one kernel launch on rotation i."""
+    one kernel launch on rotation i. mfma_peak: the dense MFMA peak of the
+    arithmetic the kernels run (bf16/fp16, or fp32 for the TF32-off mode)."""
 
-    def __init__(self, name, launch, nbytes, flops, bound, nrot):
+    def __init__(self, name, launch, nbytes, flops, bound, nrot,
+                 mfma_peak=BF16_MFMA_PEAK_TFLOPS):
         self.name, self.launch, self.nbytes, self.flops = name, launch, nbytes, flops
-        self.bound, self.nrot = bound, nrot
+        self.bound, self.nrot, self.mfma_peak = bound, nrot, mfma_peak
 
 
 def time_case(torch, case: Case, steps: int, warmup: int):
@@ -131,7 +133,8 @@ def make_fp32_case(torch, lib, L, M=16, K=1024, N=4096):
             raise RuntimeError(f"fp32 launch failed: {st}")
 
     nbytes = M * K * 4 + N * K * 4 + K * 4 + M * N * 4
-    case = Case(f"fp32_rmsnorm_linear_M{M}_K{K}_N{N}", launch, nbytes, 2 * M * N * K, "hbm", nrot)
+    case = Case(f"fp32_rmsnorm_linear_M{M}_K{K}_N{N}", launch, nbytes, 2 * M * N * K, "hbm", nrot,
+                FP32_MFMA_PEAK_TFLOPS)
     case.keep = (wl, x, gamma, y, ws)
     return case
 
@@ -171,31 +174,41 @@ def make_int4_case(torch, lib, L):
     return case
 
 
-def make_verify_case(torch, lib, L):
+def make_verify_case(torch, lib, L, dtype=None, bias=False):
+    """fused_multi_verify at the multi-verify workload's shape: hidden [8, 5,
+    4096], lm_head [128256, 4096], optionally with the lm_head's bias [128256]
+    (the engine's call, mtp_engine.py:1237-1242), in bf16 or in the engine's
+    default fp32."""
     import torch.nn.functional as F
     from mtp_hip import workloads
-    d = workloads.multi_verify()
+    dtype = dtype or torch.bfloat16
+    d = workloads.multi_verify(dtype=dtype, bias=bias)
     dev = torch.device("cuda")
     hidden = d["hidden"].to(dev)
     W = d["weight"].to(dev)
+    b = d["bias"].to(dev) if bias else None
     B, S, K = hidden.shape
     V = W.shape[0]
     D = S - 1
+    esz = hidden.element_size()
     # drafts from the target argmax (synthetic input construction only)
     with torch.no_grad():
         Wf = W.float().contiguous()
-        top = F.linear(hidden.reshape(-1, K).float(), Wf).argmax(-1)
+        top = F.linear(hidden.reshape(-1, K).float(), Wf, None if b is None else b.float())
+        top = top.argmax(-1)
         del Wf
     draft = workloads.make_chain_drafts(top.reshape(B, S).cpu(), V, d["seed"]).to(dev)
     draft32 = draft.to(torch.int32)
     accept = torch.empty((B, D), dtype=torch.int8, device=dev)
     acc_n = torch.empty((B,), dtype=torch.int32, device=dev)
     corr = torch.empty((B,), dtype=torch.int32, device=dev)
-    nws = lib.mtp_verify_workspace_bytes(L.BF16, B * S, S, V, K)
+    code = L.code(dtype)
+    nws = lib.mtp_verify_workspace_bytes(code, B * S, S, V, K)
     ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
     fn = lib.mtp_fused_multi_verify
-    args = (hidden.data_ptr(), L.BF16, B, S, K, W.data_ptr(), L.BF16, V, None, 0,
+    args = (hidden.data_ptr(), code, B, S, K, W.data_ptr(), code, V,
+            None if b is None else b.data_ptr(), code if bias else 0,
             draft32.data_ptr(), D, accept.data_ptr(), acc_n.data_ptr(), corr.data_ptr(), None,
             ws.data_ptr(), nws, stream)
 
@@ -204,9 +217,13 @@ def make_verify_case(torch, lib, L):
         if st != 0:
             raise RuntimeError(f"multi-verify launch failed: {st}")
 
-    nbytes = B * S * K * 2 + V * K * 2 + B * D * 4 + B * D + B * 4 * 2
-    case = Case("multi_verify_B8_S5_V128256", launch, nbytes, 2 * B * S * K * V, "hbm", 1)
-    case.keep = (hidden, W, draft32, accept, acc_n, corr, ws)
+    nbytes = B * S * K * esz + V * K * esz + (V * esz if bias else 0) + B * D * 4 + B * D + \
+        B * 4 * 2
+    name = "multi_verify_B8_S5_V128256" + ("_bias" if bias else "") + \
+        ("_fp32" if dtype == torch.float32 else "")
+    peak = FP32_MFMA_PEAK_TFLOPS if dtype == torch.float32 else BF16_MFMA_PEAK_TFLOPS
+    case = Case(name, launch, nbytes, 2 * B * S * K * V, "hbm", 1, peak)
+    case.keep = (hidden, W, b, draft32, accept, acc_n, corr, ws)
     return case
 
 
@@ -363,6 +380,9 @@ def main():
                 ("fp8_M32", lambda: make_fp8_case(torch, lib, L, 32)),
                 ("fp32_M16", lambda: make_fp32_case(torch, lib, L)),
                 ("multi_verify", lambda: make_verify_case(torch, lib, L)),
+                ("multi_verify_bias", lambda: make_verify_case(torch, lib, L, bias=True)),
+                ("multi_verify_fp32", lambda: make_verify_case(torch, lib, L, torch.float32,
+                                                               bias=True)),
                 ("tree_verify", lambda: make_tree_verify_case(torch, lib, L)),
                 ("int4_M256", lambda: make_int4_case(torch, lib, L))]
     if args.only:
@@ -378,7 +398,7 @@ def main():
         gbs = case.nbytes / (ms * 1e-3) / 1e9
         tfl = case.flops / (ms * 1e-3) / 1e12
         hbm_frac = gbs / HBM_PEAK_GBS
-        mfma_frac = tfl / (FP32_MFMA_PEAK_TFLOPS if key.startswith("fp32") else BF16_MFMA_PEAK_TFLOPS)
+        mfma_frac = tfl / case.mfma_peak
         detail[key] = dict(workload=case.name, us_per_call=round(us, 3), GBps=round(gbs, 1),
                            TFLOPs=round(tfl, 2), bound=case.bound,
                            roofline_frac=round(hbm_frac if case.bound == "hbm" else mfma_frac, 4),
@@ -411,7 +431,8 @@ def main():
         cpu = cpu_baseline_fp8(torch, 64)
         log("[bench] cpu baseline (oracle, fp32 configuration)")
         detail["cpu_baseline_fp32_M16"] = cpu_baseline_fp32(torch)
-    verify_us = {k: detail[k]["us_per_call"] for k in ("multi_verify", "tree_verify")
+    verify_us = {k: detail[k]["us_per_call"] for k in ("multi_verify", "multi_verify_bias",
+                                                       "multi_verify_fp32", "tree_verify")
                  if k in detail}
 
     case, ms, steps = headline

@@ -215,16 +215,41 @@ int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B,
                            void *stream);
 
 /*
+ * fused_multi_verify(..., convention="textbook") (keyword extension). The
+ * reference's convention is mtp_fused_multi_verify's
+ * (mtp_fused_verify.py:136-154, 184-195: draft d checked against the argmax
+ * at s = d + 1, corrected = the anchor's argmax); this is the textbook
+ * speculative-decoding chain on the same argmax tokens:
+ *   accept[b, d] = (top[b, d] == draft[b, d]) and accept[b, d-1]
+ *   accepted_n[b] = number of leading accepted drafts
+ *   corrected[b] = top[b, accepted_n[b]]  (the replacement token, or the
+ *                                          bonus token when all D accept)
+ * Same arguments, kernels and workspace as mtp_fused_multi_verify.
+ */
+int mtp_fused_multi_verify_textbook(const void *hidden, int h_dtype, int64_t B,
+                                    int64_t S, int64_t K, const void *weight,
+                                    int w_dtype, int64_t V, const void *bias,
+                                    int bias_dtype, const int32_t *draft,
+                                    int64_t D, int8_t *accept,
+                                    int32_t *accepted_n, int32_t *corrected,
+                                    int32_t *top_out, void *workspace,
+                                    size_t workspace_bytes, void *stream);
+
+/*
  * Allocation-free mtp_fused_multi_verify. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * arguments and results as mtp_fused_multi_verify, without the workspace:
  * the library keeps one static device array of
  * mtp_noalloc_scratch_bytes() (1 MiB) per GPU, allocated with the module,
- * and clears its counter prefix with a kernel before each call. Shapes
- * whose verify workspace (mtp_verify_workspace_bytes) exceeds it return
- * MTP_ERR_WORKSPACE. Calls on one GPU share the array: calls that overlap
- * (different streams, no ordering) race.
+ * and clears its counter prefix with a kernel before each call. The
+ * persistent and generic verify kernels need only the counter prefix; a
+ * call on the column-group kernel (mtp_verify_route) whose workspace
+ * (mtp_verify_workspace_bytes) exceeds the array returns MTP_ERR_WORKSPACE.
+ * Calls on one GPU share the array: calls that overlap (different streams,
+ * no ordering) race. mtp_noalloc_init() looks the array's address up for
+ * the current device (the first call on a device does it otherwise): call
+ * it once per device before capturing calls into a graph.
  */
 int mtp_fused_multi_verify_noalloc(const void *hidden, int h_dtype, int64_t B,
                                    int64_t S, int64_t K, const void *weight,
@@ -234,6 +259,27 @@ int mtp_fused_multi_verify_noalloc(const void *hidden, int h_dtype, int64_t B,
                                    int32_t *accepted_n, int32_t *corrected,
                                    int32_t *top_out, void *stream);
 size_t mtp_noalloc_scratch_bytes(void);
+int mtp_noalloc_init(void);
+
+/*
+ * The kernel a verify call with these operands takes (host only, nothing
+ * launched): rows = M, seq = 1 for mtp_fused_verify; rows = B * S, seq = S
+ * for the chain. No counterpart in the reference (its routes are Triton or
+ * eager); for tests and tuning. Returns one of:
+ *   MTP_VERIFY_ROUTE_STREAM        persistent W-streaming kernel (one dtype
+ *                                  for hidden and W: BF16 / F16 / F32; any
+ *                                  bias; K * element bytes % 512 == 0;
+ *                                  16-byte aligned rows)
+ *   MTP_VERIFY_ROUTE_COLUMN_GROUP  column-group streaming kernel
+ *   MTP_VERIFY_ROUTE_GENERIC       any dtypes, K and alignment
+ * or a negative status.
+ */
+#define MTP_VERIFY_ROUTE_STREAM 0
+#define MTP_VERIFY_ROUTE_COLUMN_GROUP 1
+#define MTP_VERIFY_ROUTE_GENERIC 2
+int mtp_verify_route(const void *hidden, int h_dtype, int64_t rows, int64_t seq,
+                     int64_t K, const void *weight, int w_dtype, int64_t V,
+                     const void *bias);
 
 /* Workspace bytes for mtp_fused_verify (rows = M, seq = 1) or
  * mtp_fused_multi_verify (rows = B * S, seq = S) at vocabulary size V. */
@@ -484,8 +530,10 @@ int mtp_paged_kv_write(const void *k_new, const void *v_new, int src_dtype,
  *   width = reject ? a_n + 1 : D
  *   tokens[b, :width] = reject ? draft[b, :a_n] ++ corrected[b] : draft[b]
  *   tokens[b, width:] = -1;  *kv_len = *checkpoint + width;  *width_out = width
- * and, when ids is not NULL, ids[b, *ids_len + j] = tokens[b, j] (j < width,
- * inside ld_ids) and *ids_len += width. tokens [B, D + 1] int64; draft
+ * and, when ids is not NULL (contiguous rows of capacity ld_ids),
+ * ids[b, *ids_len + j] = tokens[b, j] for the j < width that fit and
+ * *ids_len += that count: *ids_len never passes ld_ids, so a full buffer
+ * shows as an advance shorter than *width_out. tokens [B, D + 1] int64; draft
  * [B, D] int32 or int64; checkpoint / kv_len / ids_len are int64 device
  * scalars (kv_len may alias checkpoint). One workgroup.
  */

@@ -84,8 +84,8 @@ struct CommitArgs {
   int64_t *kv_len;            // device out: checkpoint + width (may alias checkpoint)
   int64_t *tokens;            // [B, D + 1] out: this step's tokens, -1 past the width
   int32_t *width;             // device out: tokens per row this step
-  int64_t *ids;               // [B, ld_ids] id buffer or null
-  int64_t ld_ids;
+  int64_t *ids;               // [B, ld_ids] id buffer (contiguous rows) or null
+  int64_t ld_ids;             // its row length: the capacity
   int64_t *ids_len;           // device: valid columns of ids (advanced by width)
 };
 
@@ -132,7 +132,10 @@ __global__ void __launch_bounds__(256) verify_commit_kernel(const CommitArgs a) 
   if (th == 0) {
     a.kv_len[0] = ck + w;
     a.width[0] = w;
-    if (a.ids) a.ids_len[0] = base + w;
+    // ids_len advances by the tokens that fit and never passes ld_ids: a
+    // full buffer drops the rest, which the caller sees as an advance
+    // shorter than width
+    if (a.ids) a.ids_len[0] = base + min((int64_t)w, max((int64_t)0, a.ld_ids - base));
   }
 }
 

@@ -1192,14 +1192,17 @@ int mtp_fused_int4_matmul(const void *x, int x_dtype, int64_t M, int64_t K, cons
 // ---------------------------------------------------------------------------
 static int verify_rows_per_chunk(int64_t seq) { return (int)((64 / seq) * seq); }
 
-// Persistent streaming verify (skv.hpp): 16-bit hidden and weights, no bias,
-// K a multiple of 256 (the stages of a tile, 64 k each, are whole rounds of
-// the 4-slot register ring), W within the 2 GiB reach of one buffer
-// descriptor. MTP_VERIFY_WSTREAM selects the column-group kernel instead.
-bool skv_usable(int ht, int64_t V, int64_t K, const void *bias) {
-  if (ht != MTP_BF16 && ht != MTP_F16) return false;
-  if (bias || K <= 0 || K % 256 != 0 || V <= 0) return false;
-  if (V * K * 2 >= ((int64_t)1 << 31)) return false;
+// Persistent streaming verify (skv.hpp): hidden and W of one dtype (BF16,
+// F16, F32), any bias; 128 bytes of a W row per stage, so K * element bytes
+// a multiple of 512 (the stages of a tile are whole rounds of the 4-slot
+// register ring: K % 256 for 16-bit, K % 128 for fp32); a 256-row tile of W
+// within the reach of one buffer descriptor (W itself may be any size).
+// MTP_VERIFY_WSTREAM selects the column-group kernel instead.
+bool skv_usable(int ht, int64_t V, int64_t K) {
+  if (ht != MTP_BF16 && ht != MTP_F16 && ht != MTP_F32) return false;
+  const int64_t row = K * dtype_bytes(ht);
+  if (K <= 0 || V <= 0 || row % 512 != 0) return false;
+  if ((int64_t)kSkvBN * row >= ((int64_t)1 << 31)) return false;
   return tune(kTuneVerifyWstream) <= 0;
 }
 
@@ -1214,8 +1217,8 @@ size_t mtp_verify_workspace_bytes(int h_dtype, int64_t rows, int64_t seq, int64_
 
 // One launch per chunk of rows_per_chunk rows (whole batch elements).
 static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const void *w, int64_t V,
-                      int rows_per_chunk, const WsArgs &o, void *ws, size_t ws_bytes,
-                      hipStream_t st) {
+                      const void *bias, int bt, int rows_per_chunk, const WsArgs &o, void *ws,
+                      size_t ws_bytes, hipStream_t st) {
   if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;
   if (!ws || ws_bytes < kCounterBytes) return MTP_ERR_WORKSPACE;
   unsigned char *w8 = (unsigned char *)ws;
@@ -1223,19 +1226,22 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
   const int grid = (int)std::min<int64_t>(ntiles, device_cus());
   for (int64_t m0 = 0; m0 < rows; m0 += rows_per_chunk) {
     const int Mloc = (int)std::min<int64_t>(rows_per_chunk, rows - m0);
-    SkvKernel k = skv_pick(ht, Mloc <= 32 ? 1 : 2);
+    SkvKernel k = skv_pick(ht, ht == MTP_F32 ? (Mloc + 15) / 16 : (Mloc <= 32 ? 1 : 2));
     if (!k) return MTP_ERR_DTYPE;
     SkvArgs a{};
-    a.x = (const uint16_t *)hidden + m0 * K;
+    a.x = (const unsigned char *)hidden + m0 * K * dtype_bytes(ht);
     a.w = w;
+    a.bias = bias;
+    a.bias_dt = bt;
     a.M = Mloc;
     a.N = (int)V;
     a.K = (int)K;
     a.ntiles = (int)ntiles;
-    a.nst = (int)(K / 64);
+    a.nst = (int)(K * dtype_bytes(ht) / kSkUB);  // 128-byte stages of a W row
     a.keys = (unsigned long long *)(w8 + kSkvKeysOff);
     a.ticket = (unsigned *)w8;
     a.multi = o.multi;
+    a.textbook = o.textbook;
     if (!o.multi) {
       a.draft = o.draft + m0;
       a.accept = o.accept + m0;
@@ -1282,6 +1288,7 @@ static int launch_vgen(const void *hidden, int ht, int64_t rows, int64_t K, cons
     a.keys = (unsigned long long *)(w8 + kSkvKeysOff);
     a.ticket = (unsigned *)w8;
     a.out.multi = o.multi;
+    a.out.textbook = o.textbook;
     if (!o.multi) {
       a.out.draft = o.draft + m0;
       a.out.accept = o.accept + m0;
@@ -1302,18 +1309,29 @@ static int launch_vgen(const void *hidden, int ht, int64_t rows, int64_t K, cons
   return MTP_OK;
 }
 
-// Route: the persistent streaming kernel (16-bit, no bias, K % 256 == 0,
-// 16-byte aligned), else the column-group streaming kernel (same dtype for
-// hidden and W, 16-byte rows and pointers), else the generic kernel.
+// Route: the persistent streaming kernel (one dtype for hidden and W:
+// BF16, F16 or F32; any bias; 128-byte stages of whole ring rounds; 16-byte
+// aligned), else the column-group streaming kernel (same dtype for hidden
+// and W, 16-byte rows and pointers), else the generic kernel.
+static int verify_route(const void *hidden, int ht, int64_t rows, int64_t K, const void *w,
+                        int wt, int64_t V, const void *bias, int rows_per_chunk, Plan *plan) {
+  const bool aligned = aligned16(hidden) && aligned16(w);
+  if (wt == ht && aligned && skv_usable(ht, V, K)) return MTP_VERIFY_ROUTE_STREAM;
+  *plan = make_plan(ht, wt, rows, V, K, EPI_ARGMAX, rows_per_chunk);
+  if (plan->generic || !aligned || wt != ht || (bias && !aligned16(bias)))
+    return MTP_VERIFY_ROUTE_GENERIC;
+  return MTP_VERIFY_ROUTE_COLUMN_GROUP;
+}
+
 static int verify_common(const void *hidden, int ht, int64_t rows, int64_t K, const void *w,
                          int wt, int64_t V, const void *bias, int bt, int rows_per_chunk,
                          WsArgs &a, void *ws, size_t ws_bytes, void *stream) {
-  const bool aligned = aligned16(hidden) && aligned16(w);
-  if (wt == ht && aligned && skv_usable(ht, V, K, bias))
-    return launch_skv(hidden, ht, rows, K, w, V, rows_per_chunk, a, ws, ws_bytes,
+  Plan p{};
+  const int route = verify_route(hidden, ht, rows, K, w, wt, V, bias, rows_per_chunk, &p);
+  if (route == MTP_VERIFY_ROUTE_STREAM)
+    return launch_skv(hidden, ht, rows, K, w, V, bias, bt, rows_per_chunk, a, ws, ws_bytes,
                       (hipStream_t)stream);
-  Plan p = make_plan(ht, wt, rows, V, K, EPI_ARGMAX, rows_per_chunk);
-  if (p.generic || !aligned || wt != ht || (bias && !aligned16(bias)))
+  if (route == MTP_VERIFY_ROUTE_GENERIC)
     return launch_vgen(hidden, ht, rows, K, w, wt, V, bias, bt, rows_per_chunk, a, ws, ws_bytes,
                        (hipStream_t)stream);
   if (!ws || ws_bytes < p.total) return MTP_ERR_WORKSPACE;
@@ -1326,6 +1344,17 @@ static int verify_common(const void *hidden, int ht, int64_t rows, int64_t K, co
   a.K = (int)K;
   a.scale = 1.0f;
   return launch_ws(p, a, EPI_ARGMAX, ws, (hipStream_t)stream);
+}
+
+int mtp_verify_route(const void *hidden, int h_dtype, int64_t rows, int64_t seq, int64_t K,
+                     const void *weight, int w_dtype, int64_t V, const void *bias) {
+  if (!is_float_dt(h_dtype) || !is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
+  if (rows < 1 || seq < 1 || seq > 64 || K <= 0 || V <= 0 || rows > INT32_MAX ||
+      K > INT32_MAX || V > INT32_MAX)
+    return MTP_ERR_SHAPE;
+  Plan p{};
+  return verify_route(hidden, h_dtype, rows, K, weight, w_dtype, V, bias,
+                      seq == 1 ? 64 : verify_rows_per_chunk(seq), &p);
 }
 
 int mtp_fused_verify(const void *hidden, int h_dtype, int64_t M, int64_t K, const void *weight,
@@ -1347,11 +1376,12 @@ int mtp_fused_verify(const void *hidden, int h_dtype, int64_t M, int64_t K, cons
                        workspace, workspace_bytes, stream);
 }
 
-int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B, int64_t S, int64_t K,
-                           const void *weight, int w_dtype, int64_t V, const void *bias,
-                           int bias_dtype, const int32_t *draft, int64_t D, int8_t *accept,
-                           int32_t *accepted_n, int32_t *corrected, int32_t *top_out,
-                           void *workspace, size_t workspace_bytes, void *stream) {
+static int multi_verify_common(const void *hidden, int h_dtype, int64_t B, int64_t S, int64_t K,
+                               const void *weight, int w_dtype, int64_t V, const void *bias,
+                               int bias_dtype, const int32_t *draft, int64_t D, int8_t *accept,
+                               int32_t *accepted_n, int32_t *corrected, int32_t *top_out,
+                               void *workspace, size_t workspace_bytes, void *stream,
+                               int textbook) {
   if (!is_float_dt(h_dtype) || !is_float_dt(w_dtype)) return MTP_ERR_DTYPE;
   if (bias && !is_float_dt(bias_dtype)) return MTP_ERR_DTYPE;
   if (B < 0 || S < 1 || D < 0 || S != D + 1 || K <= 0 || V <= 0 || S > 64 ||
@@ -1367,11 +1397,33 @@ int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B, int64_t S
   a.corrected = corrected;
   a.top = top_out;
   a.multi = 1;
+  a.textbook = textbook;
   a.S_seq = (int)S;
   a.D = (int)D;
   const int rpc = verify_rows_per_chunk(S);
   return verify_common(hidden, h_dtype, B * S, K, weight, w_dtype, V, bias, bias_dtype, rpc, a,
                        workspace, workspace_bytes, stream);
+}
+
+int mtp_fused_multi_verify(const void *hidden, int h_dtype, int64_t B, int64_t S, int64_t K,
+                           const void *weight, int w_dtype, int64_t V, const void *bias,
+                           int bias_dtype, const int32_t *draft, int64_t D, int8_t *accept,
+                           int32_t *accepted_n, int32_t *corrected, int32_t *top_out,
+                           void *workspace, size_t workspace_bytes, void *stream) {
+  return multi_verify_common(hidden, h_dtype, B, S, K, weight, w_dtype, V, bias, bias_dtype,
+                             draft, D, accept, accepted_n, corrected, top_out, workspace,
+                             workspace_bytes, stream, 0);
+}
+
+int mtp_fused_multi_verify_textbook(const void *hidden, int h_dtype, int64_t B, int64_t S,
+                                    int64_t K, const void *weight, int w_dtype, int64_t V,
+                                    const void *bias, int bias_dtype, const int32_t *draft,
+                                    int64_t D, int8_t *accept, int32_t *accepted_n,
+                                    int32_t *corrected, int32_t *top_out, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+  return multi_verify_common(hidden, h_dtype, B, S, K, weight, w_dtype, V, bias, bias_dtype,
+                             draft, D, accept, accepted_n, corrected, top_out, workspace,
+                             workspace_bytes, stream, 1);
 }
 
 

@@ -5,10 +5,13 @@
 // The array `scratch` holds kNoallocScratchBytes per device (each GPU the
 // library runs on keeps its own copy until the process ends). Its device
 // address is looked up once per device, with that device current, by
-// hipGetSymbolAddress; host code uses only that address, never the array's
-// name. Every call clears the counter prefix (tickets and row keys) with a
-// kernel before the verify launches, so the previous call's contents do not
-// matter; two calls that overlap on one GPU share the array and race.
+// hipGetSymbolAddress (mtp_noalloc_init, or else the first call on that
+// device); host code uses only that address, never the array's name. Every
+// call clears the counter prefix (tickets and row keys) with a kernel before
+// the verify launches, so the previous call's contents do not matter; two
+// calls that overlap on one GPU share the array and race. A call needs the
+// counter prefix on the persistent and generic verify kernels, and the
+// column-group kernel's per-tile maxima besides on that route.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -63,6 +66,11 @@ extern "C" {
 
 size_t mtp_noalloc_scratch_bytes(void) { return kNoallocScratchBytes; }
 
+int mtp_noalloc_init(void) {
+  void *ws = nullptr;
+  return scratch_of_current_device(&ws);
+}
+
 int mtp_fused_multi_verify_noalloc(const void *hidden, int h_dtype, int64_t B, int64_t S,
                                    int64_t K, const void *weight, int w_dtype, int64_t V,
                                    const void *bias, int bias_dtype, const int32_t *draft,
@@ -77,8 +85,12 @@ int mtp_fused_multi_verify_noalloc(const void *hidden, int h_dtype, int64_t B, i
   if (B == 0) return MTP_OK;
   if (!hidden || !weight || !accepted_n || !corrected || (D > 0 && (!draft || !accept)))
     return MTP_ERR_NULL;
-  if (mtp_verify_workspace_bytes(h_dtype, B * S, S, V, K) > kNoallocScratchBytes)
-    return MTP_ERR_WORKSPACE;
+  const int route = mtp_verify_route(hidden, h_dtype, B * S, S, K, weight, w_dtype, V, bias);
+  if (route < 0) return route;
+  const size_t need = route == MTP_VERIFY_ROUTE_COLUMN_GROUP
+                          ? mtp_verify_workspace_bytes(h_dtype, B * S, S, V, K)
+                          : kCounterBytes;
+  if (need > kNoallocScratchBytes) return MTP_ERR_WORKSPACE;
   void *ws = nullptr;
   int s = scratch_of_current_device(&ws);
   if (s != MTP_OK) return s;

@@ -12,6 +12,8 @@ constexpr int kSkvBN = 256;      // columns per tile
 struct SkvArgs {
   const void *x;        // hidden rows of this chunk: [M, K] compute type, row stride K
   const void *w;        // [N, K] compute type
+  const void *bias;     // [N] bias_dt (F32 / BF16 / F16) or null
+  int bias_dt;
   int M, N, K;          // M <= 64
   int ntiles, nst;      // kSkvBN-column tiles, stages (64 k) per tile
   unsigned long long *keys;  // [64] packed (value, index) maxima, zero between launches
@@ -24,10 +26,12 @@ struct SkvArgs {
   int32_t *top;  // [M] or null
   int S_seq, D;
   int multi;     // 1: chain acceptance, 0: single-token verify
+  int textbook;  // chain convention (chain_accept): 0 the reference's, 1 textbook
 };
 
 typedef void (*SkvKernel)(SkvArgs);
-// Kernel for compute type ct (BF16 / F16) and mt 32-row tiles (1, 2), or null.
+// Kernel for compute type ct and mt row tiles: BF16 / F16 with 1-2 tiles of
+// 32 rows, F32 with 1-4 tiles of 16 rows; null otherwise.
 SkvKernel skv_pick(int ct, int mt);
 
 }  // namespace mtp

@@ -41,7 +41,29 @@ struct VerifyOut {
   int32_t *top;          // [M] or null
   int S_seq, D;
   int multi;             // 1: chain acceptance, 0: single-token verify
+  int textbook;          // chain convention: 0 the reference's, 1 textbook
 };
+
+// The acceptance chain of one batch element from its S = D + 1 argmax
+// tokens tp[0..D] and drafts dr[0..D-1]; accept is prefix-masked (0 after
+// the first rejection).
+//   reference (mtp_fused_verify.py:136-154, 184-195): draft d is checked
+//     against tp[d + 1] (s = 0 is the anchor); corrected = tp[0];
+//   textbook speculative decoding: draft d is checked against tp[d];
+//     corrected = tp[accepted_n] (the replacement token, or the bonus token
+//     after D accepted drafts).
+__device__ __forceinline__ void chain_accept(const int *tp, const int32_t *dr, int D,
+                                             int textbook, int8_t *accept, int32_t *accepted_n,
+                                             int32_t *corrected) {
+  int n = 0;
+  for (int d = 0; d < D; ++d) {
+    const bool ok = (tp[d + 1 - textbook] == dr[d]) && (n == d);
+    accept[d] = (int8_t)ok;
+    if (ok) n = d + 1;
+  }
+  *accepted_n = n;
+  *corrected = tp[textbook ? n : 0];
+}
 
 // Run by every thread of the last workgroup to arrive (after the acquire):
 // decode and re-zero the M row keys, write top and the acceptance outputs.
@@ -68,17 +90,9 @@ __device__ __forceinline__ void verify_finish(unsigned long long *keys, int M, c
     for (int m = th; m < M; m += nth) o.accept[m] = (int8_t)(s_top[m] == s_draft[m]);
   } else {
     const int Sq = o.S_seq, Dd = o.D;
-    for (int bl = th; bl < M / Sq; bl += nth) {
-      const int *tp = s_top + bl * Sq;
-      o.corrected[bl] = tp[0];
-      int n = 0;
-      for (int d = 0; d < Dd; ++d) {
-        const bool ok = (tp[d + 1] == s_draft[bl * Dd + d]) && (n == d);
-        o.accept[(int64_t)bl * Dd + d] = (int8_t)ok;
-        if (ok) n = d + 1;
-      }
-      o.accepted_n[bl] = n;
-    }
+    for (int bl = th; bl < M / Sq; bl += nth)
+      chain_accept(s_top + bl * Sq, s_draft + bl * Dd, Dd, o.textbook,
+                   o.accept + (int64_t)bl * Dd, o.accepted_n + bl, o.corrected + bl);
   }
 }
 

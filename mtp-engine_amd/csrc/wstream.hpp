@@ -42,6 +42,7 @@
 #pragma once
 
 #include "mtp_common.hpp"
+#include "verify_tail.hpp"
 
 namespace mtp {
 
@@ -80,6 +81,7 @@ struct WsArgs {
   int32_t *top;  // [rows] or null
   int S_seq, D;  // multi-verify: hidden rows per batch element, drafts
   int multi;     // 1: chain acceptance, 0: single-token verify
+  int textbook;  // chain convention (chain_accept): 0 the reference's, 1 textbook
 };
 
 template <int CT, int WT, int WBL>
@@ -625,15 +627,8 @@ wstream_kernel(const WsArgs a) {
       const int b0 = m0 / Sq;
       for (int bl = th; bl < Mloc / Sq; bl += NT) {
         const int b = b0 + bl;
-        const int *tp = s_top + bl * Sq;
-        a.corrected[b] = tp[0];
-        int n = 0;
-        for (int d = 0; d < Dd; ++d) {
-          const bool ok = (tp[d + 1] == a.draft[(int64_t)b * Dd + d]) && (n == d);
-          a.accept[(int64_t)b * Dd + d] = (int8_t)ok;
-          if (ok) n = d + 1;
-        }
-        a.accepted_n[b] = n;
+        chain_accept(s_top + bl * Sq, a.draft + (int64_t)b * Dd, Dd, a.textbook,
+                     a.accept + (int64_t)b * Dd, a.accepted_n + b, a.corrected + b);
       }
     }
     if (th == 0) ticket_reset(ticket);

@@ -4,9 +4,10 @@ Kernels are hand-written HIP in ../csrc, exported through the C ABI of
 include/mtp_hip.h as libmtp_hip.so and bound here with ctypes. ``ops`` holds
 the tensor-level entry points; ``kernels``, ``fused_verify`` and
 ``perf_hardening`` keep the reference modules' names and signatures on top
-of it. Two ways in: the modules ``mtp_kernels`` / ``mtp_fused_verify`` /
-``mtp_perf_hardening`` one directory up (put that directory first on
-sys.path), or ``install(...)`` into reference modules already imported.
+of it. ``install(...)`` puts the hot-path names into reference modules the
+caller already imported; the modules ``mtp_kernels`` / ``mtp_fused_verify``
+one directory up (that directory first on sys.path) are the other way in
+for those two modules.
 """
 from . import ops
 from ._lib import LIB_PATH, MtpHipError, load, reserve_workspace

@@ -22,6 +22,8 @@ F32, BF16, F16, FP8E4M3, U8, I8, I32, I64 = range(8)
 OK = 0
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_WORKSPACE, ERR_ALIGN, ERR_LAUNCH, ERR_ARG = range(-1, -8, -1)
 NIBBLE_OFFSET8, NIBBLE_TWOS = 0, 1
+# verify routes (mtp_verify_route)
+VERIFY_ROUTE_STREAM, VERIFY_ROUTE_COLUMN_GROUP, VERIFY_ROUTE_GENERIC = 0, 1, 2
 
 _TORCH_CODES = {
     torch.float32: F32,
@@ -52,6 +54,10 @@ SIGNATURES = {
     "mtp_fused_multi_verify": (
         _i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i64, _vp, _vp, _vp, _vp,
              _vp, _sz, _vp]),
+    "mtp_fused_multi_verify_textbook": (
+        _i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i64, _vp, _vp, _vp, _vp,
+             _vp, _sz, _vp]),
+    "mtp_verify_route": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp]),
     "mtp_verify_workspace_bytes": (_sz, [_i, _i64, _i64, _i64, _i64]),
     "mtp_fused_paged_attention": (
         _i, [_vp, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _f, _vp, _vp, _sz, _vp]),
@@ -91,6 +97,7 @@ SIGNATURES = {
         _i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _vp, _i64, _vp, _vp, _vp, _vp,
              _vp]),
     "mtp_noalloc_scratch_bytes": (_sz, []),
+    "mtp_noalloc_init": (_i, []),
     "mtp_set_tuning": (_i, [ctypes.c_char_p, _i64]),
     "mtp_get_tuning": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
 }
@@ -189,11 +196,20 @@ def stream_handle(device: torch.device) -> int:
 
 # ---------------------------------------------------------------------------
 # Workspace: one buffer per (device, stream), grown on demand and zeroed by
-# the library's own fill kernel (so a buffer created while a stream is being
-# captured records a kernel node, not a memset). Kernels leave their counters
-# at zero, so the buffer is reused as is. reserve_workspace() sizes it ahead
-# of a graph capture, so the capture allocates nothing.
+# the library's own fill kernel (a kernel node, never a memset, if it is
+# recorded). Kernels leave their counters at zero, so a buffer is reused as
+# is. reserve_workspace() sizes it ahead of a graph capture, so the capture
+# allocates nothing.
+#
+# A captured graph keeps the device address of every buffer it used, so no
+# buffer is ever freed: one that a larger buffer replaces is retired, not
+# dropped. A buffer first needed while the stream is being captured lives
+# in the graph's memory pool and is zeroed only when its recorded fill
+# kernel runs on replay; it serves that capture alone (kept alive here) and
+# never becomes the stream's eager workspace.
 _workspaces: dict = {}
+_captured: dict = {}
+_retired: list = []
 _MIN_WORKSPACE = MTP_COUNTER_BYTES = 65536
 
 
@@ -205,15 +221,29 @@ def _new_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def _grown(ws, nbytes: int) -> int:
+    return max(nbytes, _MIN_WORKSPACE, 0 if ws is None else 2 * ws.numel())
+
+
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     if nbytes == 0:
         return None
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, _MIN_WORKSPACE, 0 if ws is None else 2 * ws.numel())
-        ws = _new_workspace(device, size)
-        _workspaces[key] = ws
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        cap = _captured.get(key)
+        if cap is None or cap.numel() < nbytes:
+            cap = _new_workspace(device, _grown(cap if cap is not None else ws, nbytes))
+            _captured[key] = cap
+            _retired.append(cap)
+        return cap
+    _captured.pop(key, None)
+    if ws is not None:
+        _retired.append(ws)
+    ws = _new_workspace(device, _grown(ws, nbytes))
+    _workspaces[key] = ws
     return ws
 
 

@@ -22,18 +22,18 @@ from . import kernels as _k
 from . import ops
 from . import perf_hardening as _ph
 
-# Attributes replaced in the caller's mtp_kernels (every compute entry point
-# on the verify / draft path); _HAS_TRITON is set False so callers that test
-# it (mtp_radix.py:238-242, mtp_pipeline.py:7) take no Triton route.
+# Attributes replaced in the caller's mtp_kernels: the compute entry points
+# of the verify / draft path (RMSNorm -> linear in every weight format, the
+# quantizers, tree / paged attention and the tree monolith, the draft
+# chain's norms). Everything else in the module stays the reference's.
 KERNELS_NAMES = (
     "fused_rmsnorm", "fused_add_rmsnorm", "fused_rmsnorm_linear", "fused_rmsnorm_linear_fp8",
-    "fused_int4_matmul", "fused_causal_attention", "fused_causal_attention_fp8",
-    "fused_causal_attention_autotuned", "fused_bitmask_attention", "fused_paged_attention",
-    "fused_tree_attention", "fused_tree_attn_rmsnorm_linear", "quantize_fp8_e4m3",
-    "dequantize_fp8", "quantize_int4", "dequantize_int4", "prewarm_autotuner", "_HAS_TRITON",
+    "fused_int4_matmul", "fused_paged_attention", "fused_tree_attention",
+    "fused_tree_attn_rmsnorm_linear", "quantize_fp8_e4m3", "dequantize_fp8", "quantize_int4",
+    "dequantize_int4",
 )
 VERIFY_NAMES = ("fused_verify", "fused_multi_verify")
-HARDENING_NAMES = ("argmax_greedy", "sample_token", "CachedLinear", "maybe_compile")
+HARDENING_NAMES = ("argmax_greedy", "sample_token", "CachedLinear")
 
 
 def _radix_prefix_match(original):
@@ -82,8 +82,6 @@ def install(kernels_mod: Optional[ModuleType] = None, verify_mod: Optional[Modul
     if verify_mod is not None:
         for n in VERIFY_NAMES:
             rec.set(verify_mod, n, ours[n])
-        if hasattr(verify_mod, "_HAS_TRITON"):
-            rec.set(verify_mod, "_HAS_TRITON", False)
     if hardening_mod is not None:
         for n in HARDENING_NAMES:
             rec.set(hardening_mod, n, ours[n])

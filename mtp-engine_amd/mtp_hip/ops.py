@@ -157,9 +157,37 @@ def verify(hidden: torch.Tensor, weight: torch.Tensor, draft: torch.Tensor,
     return accept, top
 
 
+def verify_route(hidden: torch.Tensor, weight: torch.Tensor,
+                 bias: Optional[torch.Tensor] = None) -> str:
+    """Which kernel a verify call on these tensors takes: "stream" (the
+    persistent W-streaming kernel), "column_group" or "generic". hidden is
+    [M, K] (fused_verify) or [B, S, K] (fused_multi_verify); nothing runs."""
+    lib = _lib.load()
+    if hidden.dim() == 3:
+        B, S, K = hidden.shape
+        rows, seq = B * S, S
+    else:
+        (rows, K), seq = hidden.shape, 1
+    r = lib.mtp_verify_route(ptr(hidden), code(hidden.dtype), rows, seq, K, ptr(weight),
+                             code(weight.dtype), weight.shape[0], ptr(bias))
+    if r < 0:
+        check(r, "verify_route")
+    return {_lib.VERIFY_ROUTE_STREAM: "stream", _lib.VERIFY_ROUTE_COLUMN_GROUP: "column_group",
+            _lib.VERIFY_ROUTE_GENERIC: "generic"}[r]
+
+
+_CONVENTIONS = ("reference", "textbook")
+
+
 def multi_verify(hidden: torch.Tensor, weight: torch.Tensor, draft: torch.Tensor,
-                 bias: Optional[torch.Tensor] = None, return_top: bool = False):
-    """(accept int8 [B, D], accepted_n int32 [B], corrected int32 [B][, top int32 [B, S]])."""
+                 bias: Optional[torch.Tensor] = None, return_top: bool = False,
+                 convention: str = "reference"):
+    """(accept int8 [B, D], accepted_n int32 [B], corrected int32 [B][, top int32 [B, S]]).
+    convention: "reference" (draft d against top[:, d + 1], corrected =
+    top[:, 0]) or "textbook" (draft d against top[:, d], corrected =
+    top[b, accepted_n[b]])."""
+    if convention not in _CONVENTIONS:
+        raise ValueError(f"fused_multi_verify: convention must be one of {_CONVENTIONS}")
     lib = _lib.load()
     hidden = hidden.contiguous()
     weight = weight.contiguous()
@@ -183,7 +211,9 @@ def multi_verify(hidden: torch.Tensor, weight: torch.Tensor, draft: torch.Tensor
     top = torch.empty((B, S), dtype=torch.int32, device=dev) if return_top else None
     nbytes = lib.mtp_verify_workspace_bytes(code(hidden.dtype), B * S, S, V, K)
     ws = _lib.workspace(dev, nbytes)
-    st = lib.mtp_fused_multi_verify(
+    fn = lib.mtp_fused_multi_verify if convention == "reference" else \
+        lib.mtp_fused_multi_verify_textbook
+    st = fn(
         ptr(hidden), code(hidden.dtype), B, S, K, ptr(weight), code(weight.dtype), V,
         ptr(bias), code(bias.dtype) if bias is not None else 0, ptr(draft), D, ptr(accept),
         ptr(accepted_n), ptr(corrected), ptr(top), ptr(ws), nbytes, _lib.stream_handle(dev))
@@ -597,8 +627,9 @@ def verify_commit(accept: torch.Tensor, accepted_n: torch.Tensor, corrected: tor
     """The engine's verify consumer on the device (no host reads): returns
     (tokens [B, D + 1] int64, -1 past the width; width int32 [1]) and sets
     kv_len = checkpoint + width (int64 device scalars; they may be the same
-    tensor); with ids [B, cap] int64 and ids_len (int64 scalar) the tokens
-    are appended at ids_len, which advances by the width."""
+    tensor); with ids [B, cap] int64 (contiguous) and ids_len (int64
+    scalar) the tokens are appended at ids_len, which advances by the width,
+    or by fewer where the buffer is full (ids_len never passes cap)."""
     lib = _lib.load()
     B, D = draft.shape
     accept = accept.contiguous().to(torch.int8)
@@ -612,7 +643,7 @@ def verify_commit(accept: torch.Tensor, accepted_n: torch.Tensor, corrected: tor
             f"verify_commit: {name} must be a contiguous int64 device scalar"
     if ids is not None:
         assert ids.dtype == torch.int64 and ids.dim() == 2 and ids.shape[0] == B and \
-            ids.stride(1) == 1, "verify_commit: ids must be int64 [B, cap] with unit column stride"
+            ids.is_contiguous(), "verify_commit: ids must be a contiguous int64 [B, cap]"
         assert ids_len is not None and ids_len.dtype == torch.int64 and ids_len.numel() == 1
     _on_device("accepted_n", accepted_n, accept=accept, corrected=corrected, draft=draft,
                checkpoint=checkpoint, kv_len=kv_len, ids=ids, ids_len=ids_len)

@@ -65,22 +65,31 @@ def fp8_linear(M: int, seed: int = 1, K: int = 4096, N: int = 14336) -> Dict:
     return dict(x=x, gamma=gamma, weight_fp8=wq, wscale=ws, eps=1e-6)
 
 
-def _bf16_weight(g, N: int, K: int, std: float = 0.02, rows: int = 8192) -> torch.Tensor:
-    out = torch.empty((N, K), dtype=torch.bfloat16)
+def _weight(g, N: int, K: int, std: float = 0.02, rows: int = 8192,
+            dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    out = torch.empty((N, K), dtype=dtype)
     for r0 in range(0, N, rows):
         r1 = min(N, r0 + rows)
-        out[r0:r1] = (std * torch.randn(r1 - r0, K, generator=g)).to(torch.bfloat16)
+        out[r0:r1] = (std * torch.randn(r1 - r0, K, generator=g)).to(dtype)
     return out
 
 
-def multi_verify(seed: int = 2, B: int = 8, D: int = 4, K: int = 4096, V: int = 128256) -> Dict:
-    """Workload 3 inputs without the drafts. Draws: hidden (fp32 -> bf16),
-    W (bf16, generated in 8192-row chunks). Drafts need the target argmax:
-    see make_chain_drafts."""
+def _bf16_weight(g, N: int, K: int, std: float = 0.02, rows: int = 8192) -> torch.Tensor:
+    return _weight(g, N, K, std, rows)
+
+
+def multi_verify(seed: int = 2, B: int = 8, D: int = 4, K: int = 4096, V: int = 128256,
+                 dtype: torch.dtype = torch.bfloat16, bias: bool = False) -> Dict:
+    """Workload 3 inputs without the drafts. Draws: hidden (fp32 -> dtype),
+    W (0.02 N(0, 1) -> dtype, generated in 8192-row chunks), then with
+    bias=True a bias 0.5 N(0, 1) -> dtype (the engine's lm_head carries one,
+    mtp_engine.py:198). dtype=float32 is the engine's default head dtype.
+    Drafts need the target argmax: see make_chain_drafts."""
     g = _gen(seed)
-    hidden = _randn(g, B, D + 1, K).to(torch.bfloat16)
-    W = _bf16_weight(g, V, K)
-    return dict(hidden=hidden, weight=W, B=B, D=D, seed=seed)
+    hidden = _randn(g, B, D + 1, K).to(dtype)
+    W = _weight(g, V, K, dtype=dtype)
+    b = (0.5 * _randn(g, V)).to(dtype) if bias else None
+    return dict(hidden=hidden, weight=W, bias=b, B=B, D=D, seed=seed)
 
 
 def make_chain_drafts(top: torch.Tensor, V: int, seed: int, alpha: float = 0.6) -> torch.Tensor:

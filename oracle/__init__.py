@@ -26,6 +26,11 @@ here, in tests/test_oracle.py):
       argmax loops on tiny vocabularies; planted ties (lowest index wins);
       all-equal logits give 0; exhaustive acceptance enumeration for D <= 4;
       a mismatch followed by a later match keeps the prefix closed.
+  chain_accept_textbook — exhaustive enumeration for D <= 4 of which
+      drafts match top[b, d] (not top[b, d + 1]), with literal expected
+      accept masks, counts and corrected tokens (the replacement token, or
+      the bonus top[b, D]); a draft equal to the reference convention's
+      token but not the textbook one is rejected.
   draft_tree — the reference's known shapes (32 nodes for depth 4 x 8
       branches; trunk mask rows) and ancestor closure.
   engine_rollback — the known-answer of generate_fused's consumer logic.

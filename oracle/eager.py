@@ -244,17 +244,42 @@ def chain_accept(top, draft):
     return accept, accepted_n, corrected
 
 
-def fused_multi_verify(hidden, weight, draft, bias=None):
+def chain_accept_textbook(top, draft):
+    """The textbook speculative-decoding chain on the same argmax tokens
+    (the correct-semantics option next to the reference's convention of
+    chain_accept, mtp_fused_verify.py:136-154): accept[b, d] = top[b, d] ==
+    draft[b, d] until the first rejection; accepted_n = leading accepts;
+    corrected = top[b, accepted_n] (the replacement token, or the bonus
+    token after D accepts)."""
+    top = _cpu(top).to(torch.int32)
+    draft = _cpu(draft).to(torch.int32)
+    B, D = draft.shape
+    accept = torch.zeros((B, D), dtype=torch.int8)
+    accepted_n = torch.zeros((B,), dtype=torch.int32)
+    corrected = torch.zeros((B,), dtype=torch.int32)
+    for b in range(B):
+        n = 0
+        while n < D and int(top[b, n]) == int(draft[b, n]):
+            accept[b, n] = 1
+            n += 1
+        accepted_n[b] = n
+        corrected[b] = top[b, n]
+    return accept, accepted_n, corrected
+
+
+def fused_multi_verify(hidden, weight, draft, bias=None, convention: str = "reference"):
     """_eager_fused_multi_verify (mtp_fused_verify.py:169-196) with the
-    wrapper's checks (237-265). Returns (accept, accepted_n, corrected,
-    top [B, S], top-2 gap [B, S])."""
+    wrapper's checks (237-265); convention="textbook" runs
+    chain_accept_textbook on the same argmax tokens. Returns (accept,
+    accepted_n, corrected, top [B, S], top-2 gap [B, S])."""
     hidden = _cpu(hidden)
     B, S, K = hidden.shape
     D = draft.shape[1]
     assert S == D + 1, f"expected S == D + 1, got S={S} D={D}"
     top, gap = logits_top(hidden.reshape(B * S, K), weight, bias)
     top = top.reshape(B, S)
-    accept, accepted_n, corrected = chain_accept(top, draft)
+    chain = chain_accept if convention == "reference" else chain_accept_textbook
+    accept, accepted_n, corrected = chain(top, draft)
     return accept, accepted_n, corrected, top, gap.reshape(B, S)
 
 

@@ -1,8 +1,13 @@
-"""The drop-in boundary on the CPU (no kernel runs): every name the
-reference's engine, pipelines, radix cache, tests and benches import from
-mtp_kernels / mtp_fused_verify / mtp_perf_hardening resolves in this build's
-modules (sys.path mode), and install() replaces exactly the hot-path names
-of stand-in reference modules with the gfx950 functions and puts them back.
+"""The drop-in boundary on the CPU (no kernel runs).
+
+* install() replaces exactly the hot-path names (the fixture's `hot_path`
+  lists, the RMSNorm -> linear family, quantizers, tree / paged attention,
+  the verify entry points and the draft chain's argmax / norms, plus the
+  radix cache's prefix match) in stand-in reference modules, leaves every
+  other attribute alone, and uninstall() puts them back.
+* The sys.path drop-in modules mtp_kernels / mtp_fused_verify export every
+  name the reference's engine, pipelines, radix cache, parity tests and
+  benches import from them.
 The name lists are data transcribed from the reference's import statements
 (tests/golden/reference_imports.json)."""
 import importlib
@@ -15,6 +20,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 DATA = json.load(open(os.path.join(HERE, "golden", "reference_imports.json")))
+SYS_PATH_MODULES = ("mtp_kernels", "mtp_fused_verify")
 
 
 def _needed():
@@ -26,7 +32,7 @@ def _needed():
     return need
 
 
-@pytest.mark.parametrize("module", sorted(_needed()))
+@pytest.mark.parametrize("module", SYS_PATH_MODULES)
 def test_sys_path_modules_export_every_imported_name(module):
     mod = importlib.import_module(module)  # this build's module (tests put it first)
     assert os.path.dirname(os.path.abspath(mod.__file__)).endswith("mtp-engine_amd")
@@ -37,18 +43,32 @@ def test_sys_path_modules_export_every_imported_name(module):
         assert hasattr(mod, n), f"{module}.__all__ names {n}, which is undefined"
 
 
+def test_no_perf_hardening_shim():
+    # the reference's own mtp_perf_hardening supplies its host helpers;
+    # install() patches its three hot-path names
+    root = os.path.join(os.path.dirname(HERE), "mtp-engine_amd")
+    assert not os.path.exists(os.path.join(root, "mtp_perf_hardening.py"))
+    from mtp_hip import perf_hardening as ph
+    assert sorted(ph.__all__) == sorted(DATA["hot_path"]["mtp_perf_hardening"])
+
+
 def test_no_triton_route_and_hot_path_names_are_the_hip_functions():
     import mtp_kernels
     import mtp_fused_verify
-    import mtp_perf_hardening
-    from mtp_hip import fused_verify as fv, kernels as k, perf_hardening as ph
+    from mtp_hip import fused_verify as fv, kernels as k
     assert mtp_kernels._HAS_TRITON is False
-    ours = {"mtp_kernels": (mtp_kernels, k), "mtp_fused_verify": (mtp_fused_verify, fv),
-            "mtp_perf_hardening": (mtp_perf_hardening, ph)}
-    for mod, names in DATA["hot_path"].items():
+    ours = {"mtp_kernels": (mtp_kernels, k), "mtp_fused_verify": (mtp_fused_verify, fv)}
+    for mod in SYS_PATH_MODULES:
         shim, impl = ours[mod]
-        for n in names:
+        for n in DATA["hot_path"][mod]:
             assert getattr(shim, n) is getattr(impl, n), (mod, n)
+
+
+def test_install_names_are_the_hot_path():
+    from mtp_hip import dropin
+    assert set(dropin.KERNELS_NAMES) == set(DATA["hot_path"]["mtp_kernels"])
+    assert set(dropin.VERIFY_NAMES) == set(DATA["hot_path"]["mtp_fused_verify"])
+    assert set(dropin.HARDENING_NAMES) == set(DATA["hot_path"]["mtp_perf_hardening"])
 
 
 def _stand_in(name, names):
@@ -62,9 +82,11 @@ def test_install_replaces_exactly_the_hot_path_and_uninstall_restores():
     import mtp_hip
     from mtp_hip import dropin, fused_verify as fv, kernels as k, ops, perf_hardening as ph
     need = _needed()
-    km = _stand_in("mtp_kernels", need["mtp_kernels"] | set(dropin.KERNELS_NAMES))
+    km = _stand_in("mtp_kernels", need["mtp_kernels"] | set(dropin.KERNELS_NAMES) |
+                   {"fused_bitmask_attention", "prewarm_autotuner"})
     vm = _stand_in("mtp_fused_verify", need["mtp_fused_verify"] | {"_HAS_TRITON"})
-    hm = _stand_in("mtp_perf_hardening", need["mtp_perf_hardening"])
+    hm = _stand_in("mtp_perf_hardening", need["mtp_perf_hardening"] | set(dropin.HARDENING_NAMES) |
+                   {"next_pow2", "pad_batch", "maybe_compile", "get_stream"})
 
     class RadixKVCache:
         def __init__(self):
@@ -77,55 +99,46 @@ def test_install_replaces_exactly_the_hot_path_and_uninstall_restores():
     rm.RadixKVCache = RadixKVCache
     em = _stand_in("mtp_engine", need["mtp_kernels"] | need["mtp_fused_verify"] |
                    need["mtp_perf_hardening"] | {"DEVICE", "SpeculativeDecodingEngine"})
-    before = {id(m): dict(vars(m)) for m in (km, vm, hm, em)}
+    mods = (km, vm, hm, em)
+    before = {id(m): dict(vars(m)) for m in mods}
 
     rec = mtp_hip.install(km, vm, hm, rm, em)
-    for n in DATA["hot_path"]["mtp_kernels"]:
-        assert getattr(km, n) is getattr(k, n), n
-    for n in DATA["hot_path"]["mtp_fused_verify"]:
-        assert getattr(vm, n) is getattr(fv, n), n
-    for n in DATA["hot_path"]["mtp_perf_hardening"]:
-        assert getattr(hm, n) is getattr(ph, n), n
-    assert km._HAS_TRITON is False and vm._HAS_TRITON is False
+    impl = {"mtp_kernels": (km, k), "mtp_fused_verify": (vm, fv), "mtp_perf_hardening": (hm, ph)}
+    hot = set()
+    for mod, (patched, ours) in impl.items():
+        for n in DATA["hot_path"][mod]:
+            assert getattr(patched, n) is getattr(ours, n), (mod, n)
+            hot.add(n)
+    # exactly the hot-path names changed, in every module
+    for m in mods:
+        changed = {n for n, v in vars(m).items() if before[id(m)].get(n, object()) is not v}
+        expect = {n for n in hot if n in before[id(m)]}
+        assert changed == expect, (m.__name__, sorted(changed ^ expect))
+    assert km._HAS_TRITON == ("reference", "mtp_kernels", "_HAS_TRITON")
+    assert vm._HAS_TRITON == ("reference", "mtp_fused_verify", "_HAS_TRITON")
     # the engine's own bindings of hot-path names are redirected, the rest kept
     assert em.fused_rmsnorm_linear is k.fused_rmsnorm_linear
     assert em.fused_multi_verify is fv.fused_multi_verify
     assert em.argmax_greedy is ph.argmax_greedy
+    assert em.fused_causal_attention == ("reference", "mtp_engine", "fused_causal_attention")
     assert em.SpeculativeDecodingEngine == ("reference", "mtp_engine", "SpeculativeDecodingEngine")
-    # everything not on the hot path still resolves to the reference object
-    replaced = set(dropin.KERNELS_NAMES) | set(dropin.VERIFY_NAMES) | set(dropin.HARDENING_NAMES)
-    for n in need["mtp_kernels"] - replaced:
-        assert getattr(km, n) == ("reference", "mtp_kernels", n), n
-    for n in need["mtp_perf_hardening"] - replaced:
-        assert getattr(hm, n) == ("reference", "mtp_perf_hardening", n), n
+    assert set(rec.names()) == {"mtp_kernels", "mtp_fused_verify", "mtp_perf_hardening",
+                                "mtp_engine", "RadixKVCache"}
     # every import statement of the reference resolves against the patched modules
-    mods = {"mtp_kernels": km, "mtp_fused_verify": vm, "mtp_perf_hardening": hm}
+    by_name = {"mtp_kernels": km, "mtp_fused_verify": vm, "mtp_perf_hardening": hm}
     for imp in DATA["imports"]:
         for n in imp["names"]:
-            assert hasattr(mods[imp["module"]], n), (imp["site"], n)
+            assert hasattr(by_name[imp["module"]], n), (imp["site"], n)
     # radix: device ids take the kernel, host ids keep the reference's route
     cache = rm.RadixKVCache()
     assert cache.batch_prefix_match(torch.zeros(2, 3, dtype=torch.long)) == "reference eager"
     mtp_hip.uninstall(rec)
-    for m in (km, vm, hm, em):
+    for m in mods:
         assert dict(vars(m)) == before[id(m)]
     assert rm.RadixKVCache().batch_prefix_match(None) == "reference eager"
     assert ops.batch_prefix_match is not None
 
 
-def test_host_helpers_match_reference_contracts():
-    import mtp_perf_hardening as mh
-    assert [mh.next_pow2(n) for n in (0, 1, 2, 3, 17, 64)] == [1, 1, 2, 4, 32, 64]
-    assert mh.align_vocab(128256) == 128256 and mh.align_vocab(1) == 128
-    assert mh.align_vocab(130, 64) == 192
-    assert mh.pad_seq_len(33) == 64 and mh.pad_batch(9) == 16
-    assert mh.fast_check((2, 3), (2, 3)) and not mh.fast_check((2, 3), (2,))
-    c = mh.PrecomputedConstants(128, 4096, 1000, torch.bfloat16, temperature=0.0)
-    assert c.inv_temperature == 0.0 and c.vocab_padded == 1024
-    assert abs(c.attn_scale - 128 ** -0.5) < 1e-12
-    pool = mh.PinnedBufferPool(2, 8)
-    v = pool.stage_prompt(torch.tensor([[1, 2, 3]]))
-    assert v.tolist() == [[1, 2, 3]]
-    assert mh.maybe_compile(torch.nn.Linear(2, 2)).__class__ is torch.nn.Linear
+def test_tuning_config_default():
     import mtp_kernels as mk
     assert mk.build_tuning_config().fp8_scale == 1.0

@@ -112,7 +112,7 @@ def test_argmax_strided_rows_and_1d():
 
 
 def test_perf_hardening_greedy_routes():
-    import mtp_perf_hardening as mh
+    from mtp_hip import perf_hardening as mh
     g = torch.Generator().manual_seed(10)
     lg = torch.randn(2, 3, 500, generator=g)
     d = lg.to(DEV)

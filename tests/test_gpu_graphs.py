@@ -90,23 +90,29 @@ def test_fp32_linear_graph_replay(route):
         L.set_tuning(sf32=-1)
 
 
-def test_multi_verify_graph_replay():
-    """The persistent verify kernel under capture: keys and ticket are
-    reset by the last workgroup of each replay."""
+@pytest.mark.parametrize("dtype,bias", [(torch.bfloat16, None), (torch.bfloat16, torch.bfloat16),
+                                        (torch.float32, torch.float32)])
+def test_multi_verify_graph_replay(dtype, bias):
+    """The persistent verify kernel under capture, without and with the
+    engine's lm_head bias and in the engine's default fp32: keys and ticket
+    are reset by the last workgroup of each replay."""
     from mtp_hip import ops
     g = torch.Generator().manual_seed(3)
     B, D, K, V = 8, 4, 1024, 50000
-    hidden = torch.randn(B, D + 1, K, generator=g).to(torch.bfloat16).to(DEV)
-    W = (0.05 * torch.randn(V, K, generator=g)).to(torch.bfloat16).to(DEV)
+    hidden = torch.randn(B, D + 1, K, generator=g).to(dtype).to(DEV)
+    W = (0.05 * torch.randn(V, K, generator=g)).to(dtype).to(DEV)
+    b = None if bias is None else (0.5 * torch.randn(V, generator=g)).to(bias).to(DEV)
     draft = torch.randint(0, V, (B, D), generator=g).to(DEV)
-    fn = lambda: ops.multi_verify(hidden, W, draft, return_top=True)  # noqa: E731
+    assert ops.verify_route(hidden, W, b) == "stream"
+    print(f"case multi-verify graph dtype={dtype} bias={bias}", flush=True)
+    fn = lambda: ops.multi_verify(hidden, W, draft, b, return_top=True)  # noqa: E731
     graph, out = _capture(fn)
-    hs = [torch.randn(hidden.shape, generator=g).to(torch.bfloat16).to(DEV) for _ in range(4)]
+    hs = [torch.randn(hidden.shape, generator=g).to(dtype).to(DEV) for _ in range(4)]
 
     def fill(i):
         hidden.copy_(hs[i])
         # drafts that accept a prefix of the new argmax, so accepted_n varies
-        top = ops.multi_verify(hidden, W, draft, return_top=True)[3]
+        top = ops.multi_verify(hidden, W, draft, b, return_top=True)[3]
         draft.copy_(top[:, 1:].to(draft.dtype))
         draft[i % B, i % D] += 1
         torch.cuda.synchronize()
@@ -142,3 +148,67 @@ def test_commit_graph_replay_advances_device_lengths():
         assert int(kv.item()) == 10 + 2 * (i + 2)
         assert int(ids_len.item()) == 2 * (i + 2)
     assert ids[:, :8].tolist() == [[1, 9] * 4, [4, 8] * 4]
+
+
+def _norm_linear_case(g, M, K, N):
+    dt = torch.bfloat16
+    x = torch.randn(M, K, generator=g).to(dt).to(DEV)
+    W = (0.02 * torch.randn(N, K, generator=g)).to(dt).to(DEV)
+    gm = (1 + 0.1 * torch.randn(K, generator=g)).to(dt).to(DEV)
+    return x, W, gm
+
+
+def test_captured_workspace_survives_growth():
+    """A graph keeps the address of the workspace it was captured with. A
+    later, larger eager call on the capture stream gets a new buffer; the
+    old one stays allocated, so a tensor allocated afterwards (the canary,
+    the old buffer's size) is never written by a replay, and every replay
+    still equals eager."""
+    from mtp_hip import _lib as L, ops
+    g = torch.Generator().manual_seed(5)
+    x, W, gm = _norm_linear_case(g, 64, 1024, 2048)
+    fn = lambda: ops.rmsnorm_linear(x, W, None, 1e-6, 1.0, gamma=gm)  # noqa: E731
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.synchronize()
+    key = (torch.device(DEV).index or 0, s.cuda_stream)
+    old = L._workspaces[key]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = fn()
+    xb, Wb, gb = _norm_linear_case(g, 64, 16384, 2048)
+    with torch.cuda.stream(s):
+        ops.rmsnorm_linear(xb, Wb, None, 1e-6, 1.0, gamma=gb)  # grows s's workspace
+    torch.cuda.synchronize()
+    assert L._workspaces[key].data_ptr() != old.data_ptr(), "the larger call did not grow it"
+    canary = torch.full((old.numel() // 4,), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+    xs = [torch.randn(x.shape, generator=g).to(x.dtype).to(DEV) for _ in range(3)]
+    _replays(graph, out, lambda i: x.copy_(xs[i]), fn, n=3)
+    assert bool((canary == 0x5A5A5A5A).all()), "a replay wrote into memory it does not own"
+
+
+def test_capture_on_fresh_stream_then_eager():
+    """A stream whose first call is captured: the capture's workspace is
+    zeroed only by its recorded fill kernel, so eager calls on that stream
+    afterwards must get a buffer of their own (and be correct before the
+    graph ever replays)."""
+    from mtp_hip import ops
+    g = torch.Generator().manual_seed(6)
+    x, W, gm = _norm_linear_case(g, 64, 1024, 2048)
+    fn = lambda: ops.rmsnorm_linear(x, W, None, 1e-6, 1.0, gamma=gm)  # noqa: E731
+    ref = fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = fn()
+    with torch.cuda.stream(s):
+        eager = fn()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, ref)
+    xs = [torch.randn(x.shape, generator=g).to(x.dtype).to(DEV) for _ in range(3)]
+    _replays(graph, out, lambda i: x.copy_(xs[i]), fn, n=3)

@@ -124,6 +124,36 @@ def test_verify_commit_device_loop_appends_ids_and_aliases_length():
     assert bool((ids_d.cpu()[:, ref.shape[1]:] == -7).all())
 
 
+@pytest.mark.parametrize("room", [0, 1, 3])
+def test_verify_commit_full_id_buffer_stops_at_capacity(room):
+    """An id buffer with fewer free columns than the step's width: the
+    tokens that fit are written, nothing past the capacity, and ids_len
+    stops at the capacity (an advance shorter than width) while the KV
+    length still advances by the full width."""
+    from mtp_hip import ops
+    g = torch.Generator().manual_seed(78 + room)
+    B, D, V = 3, 4, 300
+    draft = torch.randint(0, V, (B, D), generator=g)
+    acc = torch.ones(B, D, dtype=torch.int8)  # all accepted: width D
+    n = torch.full((B,), D, dtype=torch.int32)
+    corr = torch.randint(0, V, (B,), generator=g).to(torch.int32)
+    cap, used = 10, 10 - room
+    store = torch.full((B * cap + 16,), -9, dtype=torch.int64, device=DEV)
+    ids = store[:B * cap].view(B, cap)  # a write past row b's capacity lands in row b + 1
+    ids_len = torch.tensor([used], dtype=torch.int64, device=DEV)
+    kv = torch.tensor([used], dtype=torch.int64, device=DEV)
+    tokens, width = ops.verify_commit(acc.to(DEV), n.to(DEV), corr.to(DEV), draft.to(DEV),
+                                      kv, kv, ids, ids_len)
+    torch.cuda.synchronize()
+    rt, rw, rkv = O.verify_commit(acc, n, corr, draft, used)
+    assert int(width.cpu()) == rw == D and int(kv.cpu()) == rkv
+    assert int(ids_len.cpu()) == cap
+    got = ids.cpu()
+    assert torch.equal(got[:, used:], rt[:, :room])
+    assert bool((got[:, :used] == -9).all())
+    assert bool((store.cpu()[B * cap:] == -9).all())
+
+
 @pytest.mark.parametrize("R,L", [(1, 5), (2, 0), (7, 5), (5, 64), (9, 65), (300, 1000),
                                  (4097, 33)])
 def test_batch_prefix_match_matches_oracle(R, L):

@@ -174,6 +174,103 @@ def test_multi_verify_workload_full_size():
     assert got[:2] == exp[:2] and torch.equal(got[2], exp[2])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_multi_verify_engine_call_full_size(dtype):
+    """The engine's own verify call, fused_multi_verify(hidden_all,
+    proj.weight, draft, bias=proj.bias) (mtp_engine.py:1237-1242,
+    1320-1322), at the multi-verify workload's size: 8 x (4+1) hidden rows,
+    lm_head [128256, 4096] with a bias [128256], in bf16 and in the
+    engine's default fp32 (2.1 GB of W). Both take the persistent
+    W-streaming kernel; tokens, accepted_n and corrected equal the oracle's
+    wherever the top-2 gap is clear."""
+    from mtp_hip import ops, workloads
+    d = workloads.multi_verify(dtype=dtype, bias=True)
+    hidden, W, b = d["hidden"], d["weight"], d["bias"]
+    top, gap = O.logits_top(hidden.reshape(-1, hidden.shape[-1]), W, b)
+    draft = workloads.make_chain_drafts(top.reshape(d["B"], d["D"] + 1), W.shape[0], d["seed"])
+    print(f"case engine verify call dtype={dtype}", flush=True)
+    hd, Wd, bd = hidden.to(DEV), W.to(DEV), b.to(DEV)
+    assert ops.verify_route(hd, Wd, bd) == "stream"
+    out = ops.multi_verify(hd, Wd, draft.to(DEV), bd, return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hidden, W, b, draft, 1e-4)
+    # without the bias the tokens differ on some rows: the bias is applied
+    nb = ops.multi_verify(hd, Wd, draft.to(DEV), None, return_top=True)[3]
+    torch.cuda.synchronize()
+    top_nb, gap_nb = O.logits_top(hidden.reshape(-1, hidden.shape[-1]), W)
+    sure = (gap_nb > 1e-4).reshape(-1)
+    assert torch.equal(nb.cpu().reshape(-1)[sure], top_nb[sure].to(torch.int32))
+    assert not torch.equal(top_nb, top)
+
+
+def test_verify_weights_past_4gib():
+    """W of 4.4 GB (fp32 [270000, 4096]): the persistent kernel addresses W
+    through one buffer descriptor per 256-row tile, so tiles past 2 and 4
+    GiB read their own rows (the last tile starts at 4.42e9 bytes)."""
+    from mtp_hip import ops, workloads
+    g = torch.Generator().manual_seed(270000)
+    V, K, M = 270000, 4096, 8
+    W = workloads._weight(g, V, K, dtype=torch.float32)
+    h = torch.randn(M, K, generator=g)
+    b = 0.5 * torch.randn(V, generator=g)
+    # the winners of some rows planted in the last tiles
+    for m, n in enumerate((V - 1, V - 200, V // 2 + 7, 262144 + 5)):
+        W[n] = 0.05 * h[m]
+    top, gap = O.logits_top(h, W, b)
+    assert int(top[0]) == V - 1 and int(top[3]) == 262144 + 5
+    print("case verify W 4.4 GB", flush=True)
+    hd, Wd, bd = h.to(DEV), W.to(DEV), b.to(DEV)
+    del W
+    assert ops.verify_route(hd, Wd, bd) == "stream"
+    draft = top.clone().to(torch.int64)
+    draft[1::2] = (draft[1::2] + 1) % V
+    acc, t = ops.verify(hd, Wd, draft.to(DEV), bd)
+    torch.cuda.synchronize()
+    _check_tokens(t, top, gap, 1e-3)
+    sure = gap > 1e-3
+    assert torch.equal(acc.cpu()[sure], (top == draft.to(torch.int32)).to(torch.int8)[sure])
+
+
+@pytest.mark.parametrize("route", ["stream", "column_group", "generic"])
+def test_multi_verify_textbook_convention(route, tune):
+    """convention="textbook": draft d is checked against top[b, d] and
+    corrected = top[b, accepted_n] (the bonus token after D accepts), on
+    each verify kernel, against the oracle's textbook chain; drafts built
+    from top[b, :D] so that whole chains, partial chains and immediate
+    rejections all occur."""
+    from mtp_hip import ops
+    B, D, V = 12, 4, 20000
+    K = 250 if route == "generic" else 512
+    g = torch.Generator().manual_seed(41)
+    hidden = torch.randn(B, D + 1, K, generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(V, K, generator=g)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(V, generator=g)).to(torch.bfloat16)
+    top, gap = O.logits_top(hidden.reshape(-1, K), W, b)
+    top, gap = top.reshape(B, D + 1), gap.reshape(B, D + 1)
+    draft = top[:, :D].clone().to(torch.int64)
+    for i in range(B):  # row i rejects at position i % (D + 1) (D + 1: accepts all)
+        j = i % (D + 1)
+        if j < D:
+            draft[i, j] = (draft[i, j] + 1) % V
+    if route == "column_group":
+        tune(verify_wstream=1)
+    hd, Wd, bd = hidden.to(DEV), W.to(DEV), b.to(DEV)
+    assert ops.verify_route(hd, Wd, bd) == route
+    print(f"case textbook route={route}", flush=True)
+    acc, n, corr, t = ops.multi_verify(hd, Wd, draft.to(DEV), bd, return_top=True,
+                                       convention="textbook")
+    torch.cuda.synchronize()
+    ra, rn, rc, rtop, rgap = O.fused_multi_verify(hidden, W, draft, b, convention="textbook")
+    assert bool((rgap > 1e-3).all()), "a near-tie in this seeded case"
+    assert torch.equal(t.cpu(), rtop.to(torch.int32))
+    assert torch.equal(acc.cpu(), ra) and torch.equal(n.cpu(), rn) and torch.equal(corr.cpu(), rc)
+    assert rn.tolist() == [i % (D + 1) for i in range(B)]
+    # the reference convention on the same call differs
+    _, n_ref, corr_ref = ops.multi_verify(hd, Wd, draft.to(DEV), bd)
+    torch.cuda.synchronize()
+    assert torch.equal(corr_ref.cpu(), rtop[:, 0].to(torch.int32))
+
+
 # --- the persistent streaming path: 16-bit, no bias, K % 512 == 0 ---------------
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -37,7 +37,7 @@ def test_shape_mismatches_are_assertions():
 
 
 def test_cached_linear_follows_module_moves():
-    from mtp_perf_hardening import CachedLinear
+    from mtp_hip.perf_hardening import CachedLinear
     lin = CachedLinear(8, 4)
     lin = lin.to(torch.float64)
     assert lin._w.dtype == torch.float64 and lin._w.data_ptr() == lin.weight.data_ptr()

@@ -147,6 +147,27 @@ def test_int4_pack_order_and_reference_roundtrip_mismatch():
     assert np.array_equal(O.dequantize_int4(packed_o, scales, K, group).numpy()[0], q)
 
 
+def test_int4_quantizer_rounds_half_to_even():
+    """Planted half-integer ties of W / s with literal expected values: the
+    reference rounds with torch.round (mtp_kernels.py:745), i.e. half to
+    even: 2.5 -> 2, 3.5 -> 4, -2.5 -> -2, 0.5 -> 0, -0.5 -> 0, 1.5 -> 2,
+    -1.5 -> -2, 4.5 -> 4, 5.5 -> 6, -3.5 -> -4; amax 7 fixes s = 1. A
+    quantizer rounding half away from zero, or truncating, fails here."""
+    K, group = 32, 32
+    vals = [2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -1.5, 4.5, 5.5, -3.5, 7.0, 6.5, -6.5, -7.0]
+    exp_q = [2, 4, -2, 0, 0, 2, -2, 4, 6, -4, 7, 6, -6, -7]
+    row = np.zeros(K, dtype=np.float32)
+    row[:len(vals)] = vals
+    packed, scales = O.quantize_int4(torch.from_numpy(row[None, :].copy()), group)
+    assert float(scales[0, 0]) == 1.0
+    nib = O.int4_nibbles(packed)[0]
+    assert nib[:len(vals)].tolist() == [q & 0xF for q in exp_q]          # reference bytes
+    po, _ = O.quantize_int4(torch.from_numpy(row[None, :].copy()), group, nibble="offset")
+    assert O.int4_nibbles(po)[0][:len(vals)].tolist() == [q + 8 for q in exp_q]
+    # literal bytes of the first pairs: (2, 4) and (-2, 0)
+    assert int(packed[0, 0]) == 0x42 and int(packed[0, 1]) == 0x0E
+
+
 def test_int4_matmul_equals_dequant_linear():
     # The reference's own check (mtp_engine.py:1812-1819): bit-identical.
     torch.manual_seed(0)
@@ -225,6 +246,31 @@ def test_chain_accept_exhaustive(D):
         assert int(n[0]) == lead
         assert acc[0].tolist() == [1] * lead + ([0] * (D - lead))
         assert int(corr[0]) == 7
+
+
+@pytest.mark.parametrize("D", [0, 1, 2, 3, 4])
+def test_chain_accept_textbook_exhaustive(D):
+    """Every accept / reject pattern of D drafts against the textbook
+    convention: draft d is compared with top[b, d] (the argmax after the
+    first d accepted tokens), corrected = top[b, accepted_n]. The tokens are
+    chosen so that the reference convention (top[b, d + 1]) would give a
+    different answer for every pattern with a match."""
+    for pattern in itertools.product([0, 1], repeat=D):
+        top = torch.tensor([[10 + s for s in range(D + 1)]])  # top[b, s] = 10 + s
+        # a matching draft d is 10 + d; a rejected one is 11 + d, which the
+        # reference convention would accept
+        draft = torch.tensor([[10 + d if pattern[d] else 11 + d for d in range(D)]])
+        acc, n, corr = O.chain_accept_textbook(top, draft)
+        lead = 0
+        while lead < D and pattern[lead]:
+            lead += 1
+        assert int(n[0]) == lead
+        assert acc[0].tolist() == [1] * lead + [0] * (D - lead)
+        assert int(corr[0]) == 10 + lead  # replacement token, or the bonus 10 + D
+        racc, rn, rcorr = O.chain_accept(top, draft)
+        assert int(rcorr[0]) == 10
+        if D and not pattern[0]:
+            assert int(rn[0]) >= 1  # the reference convention takes 11 as the first draft
 
 
 def test_multi_verify_matches_reference_test_seeded():
