@@ -172,13 +172,13 @@ skv_kernel(const SkvArgs a) {
       *(u32x4 *)(lds_w + buf * WST + (wave + 8 * v) * 1024 + lane * 16) = wr[slot][v];
     if (xloader) *(u32x4 *)(lds_x + buf * XST + xlds) = xr[slot];
   };
-  // this wave's 32 columns against all rows, the KS compute steps of the
-  // stage in buffer `buf`; the NV loads of the stage NS - 1 ahead spread
-  // over them
-  auto compute = [&](int buf, auto nslotc) __attribute__((always_inline)) {
+  // this wave's 32 columns against all rows, compute steps J0 .. J1 - 1 of
+  // the stage in buffer `buf`; the NV loads of the stage NS - 1 ahead spread
+  // over the KS steps
+  auto compute = [&](int buf, auto nslotc, auto j0c, auto j1c) __attribute__((always_inline)) {
     const unsigned char *wb = lds_w + buf * WST;
     const unsigned char *xb = lds_x + buf * XST;
-    static_for<0, KS>([&](auto jc) {
+    static_for<decltype(j0c)::value, decltype(j1c)::value>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       static_for<j * NV / KS, (j + 1) * NV / KS>([&](auto vc) { issue(vc, nslotc); });
       if constexpr (F32) {
@@ -214,7 +214,6 @@ skv_kernel(const SkvArgs a) {
         }
       }
     });
-    advance();
   };
 
   // Column (within a tile) of this lane's value q (q < NQ), the same for
@@ -273,12 +272,21 @@ skv_kernel(const SkvArgs a) {
   });
   to_lds(std::integral_constant<int, 0>{}, 0);
   lds_barrier();
+  // 16-bit: stage s + 1 goes to LDS first, then the stage's MFMAs. fp32
+  // (MFMA-bound): the first compute step's MFMAs are issued before the
+  // wait for stage s + 1's loads and its LDS stores, so the MFMA pipe has
+  // queued work while the wave waits on memory.
   auto step = [&](auto rc, int s) __attribute__((always_inline)) {
     constexpr int r = decltype(rc)::value;  // s % NS
+    using nslot = std::integral_constant<int, (r + NS - 1) % NS>;
+    constexpr int JS = F32 ? 1 : 0;  // compute steps before the LDS stores
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s & 1, nslot{}, std::integral_constant<int, 0>{}, std::integral_constant<int, JS>{});
     __builtin_amdgcn_sched_barrier(0);
     if (s + 1 < total) to_lds(std::integral_constant<int, (r + 1) % NS>{}, (s + 1) & 1);
     __builtin_amdgcn_sched_barrier(0);
-    compute(s & 1, std::integral_constant<int, (r + NS - 1) % NS>{});
+    compute(s & 1, nslot{}, std::integral_constant<int, JS>{}, std::integral_constant<int, KS>{});
+    advance();
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
   };
