@@ -57,6 +57,7 @@ enum TuneKey {
   kTuneSkpH8,            // MTP_SKP_H8: compact x blocks of the x-resident kernel (<= 8 rows), 0 off
   kTuneAttn32,           // MTP_ATTN32: 32-query-tile attention (33 .. 64 queries, D 128), 0 off
   kTuneSkXraw,           // MTP_SK_XRAW: 0 keeps sk's prep launch without gamma (default: raw x)
+  kTuneSkw,              // MTP_SKW: wave-specialised skinny kernel, 1 force where it applies, 0 off
   kTuneCount
 };
 int tune(TuneKey k);

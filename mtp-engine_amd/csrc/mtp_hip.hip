@@ -19,6 +19,7 @@
 #include "skl_args.hpp"
 #include "skp_args.hpp"
 #include "skv_args.hpp"
+#include "skw_args.hpp"
 #include "vgen.hpp"
 #include "ws_dispatch.hpp"
 
@@ -30,7 +31,8 @@ std::atomic<int> g_tune[kTuneCount];
 std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
-    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw"};
+    "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw",
+    "skw"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -64,6 +66,7 @@ void tune_init() {
   g_tune[kTuneSkpH8].store(env_int("MTP_SKP_H8", -1), std::memory_order_relaxed);
   g_tune[kTuneAttn32].store(env_int("MTP_ATTN32", -1), std::memory_order_relaxed);
   g_tune[kTuneSkXraw].store(env_int("MTP_SK_XRAW", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkw].store(env_int("MTP_SKW", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -373,7 +376,7 @@ int launch_wsp(const PlanX &p, WsArgs &a, void *ws, hipStream_t st) {
 struct PlanSk {
   bool ok = false;
   int ct = 0, wt = 0, mt = 0;
-  bool gam = false, xr = false;
+  bool gam = false, xr = false, skw = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
   int ch = 1, nsl = 0;  // prep form: 256 ch k per prep slice, slices
   size_t xf_off = 0, pss_off = 0, part_off = 0, ss_off = 0, total = 0;
@@ -388,11 +391,13 @@ constexpr int kSkMinStages = 4;    // stages per split at least
 // to its fp32 sums (no prep launch; tuning key sk_xraw 0 keeps the prep).
 // Workspace: counters, the xn blocks (prep form), split-K partials (and the
 // splits' sums of squares in the raw form).
-PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
+PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam,
+                    bool skw = false) {
   PlanSk p;
   p.ct = ct;
   p.wt = wt;
   p.gam = gam;
+  p.skw = skw;
   if (ct != MTP_BF16 && ct != MTP_F16) return p;
   if (wt != MTP_FP8E4M3 && wt != ct) return p;
   // 17 .. 64 rows: the row-chunk kernel (wsp) is faster below that
@@ -410,11 +415,13 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
   // raw x whenever there is no gamma (bf16 64 x 4096 x 4096: 14.5 us
   // against 16.3 with the prep; bf16 32 x 4096 x 4096: 12.0 against 14.5;
   // fp8 64 x 14336 x 4096: 25.1 either way)
-  p.xr = !gam && tune(kTuneSkXraw) != 0;
+  p.xr = !gam && tune(kTuneSkXraw) != 0 && !skw;
   p.G = (int)((N + kSkBN - 1) / kSkBN);
   p.nkb = (int)(K * wb / kSkUB);
   int S = 1;
-  if (forced) {
+  if (skw) {
+    S = 1;  // the wave-specialised GEMM has no K-splits
+  } else if (forced) {
     S = force;
   } else {
     while ((int64_t)p.G * S < sk_min_blocks() && p.nkb / (S + 1) >= kSkMinStages) ++S;
@@ -448,7 +455,7 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
     }
   }
   p.total = off;
-  p.ok = sk_pick(ct, wt, p.mt, p.xr) != nullptr &&
+  p.ok = (skw ? skw_pick(ct, wt, p.mt) != nullptr : sk_pick(ct, wt, p.mt, p.xr) != nullptr) &&
          (p.xr || sk_prep8_pick(ct, wt, gam, p.ch) != nullptr);
   return p;
 }
@@ -456,7 +463,7 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam) {
 int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int norm,
               SkArgs &a, void *ws, hipStream_t st) {
   SkKernel k = sk_pick(p.ct, p.wt, p.mt, p.xr);
-  if (!k) return MTP_ERR_DTYPE;
+  if (!k && !p.skw) return MTP_ERR_DTYPE;
   unsigned char *w8 = (unsigned char *)ws;
   if (p.xr) {
     a.x = x;
@@ -483,6 +490,28 @@ int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int
     a.nsl = p.nsl;
     a.norm = norm;
     a.eps = eps;
+  }
+  if (p.skw) {
+    SkwKernel kw = skw_pick(p.ct, p.wt, p.mt);
+    if (!kw) return MTP_ERR_DTYPE;
+    SkwArgs wa{};
+    wa.xf = a.xf;
+    wa.pss = a.pss;
+    wa.nsl = a.nsl;
+    wa.norm = a.norm;
+    wa.eps = a.eps;
+    wa.w = a.w;
+    wa.wscale = a.wscale;
+    wa.bias = a.bias;
+    wa.bias_dt = a.bias_dt;
+    wa.y = a.y;
+    wa.M = a.M;
+    wa.N = a.N;
+    wa.K = a.K;
+    wa.scale = a.scale;
+    wa.nst = p.nkb;
+    hipLaunchKernelGGL(kw, dim3((unsigned)p.G), dim3(512), 0, st, wa);
+    return launch_status();
   }
   a.G = p.G;
   a.S = p.S;
@@ -798,6 +827,36 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
       pa.eps = eps;
       pa.scale = scale;
       return launch_skp(pp, pa, ws, st);
+    }
+  }
+  // wave-specialised skinny GEMM (after the prep launch): by default for
+  // 33 .. 64 rows with gamma where the 64-column tiles alone fill most of
+  // the CUs (no K-split); tuning key skw 1 forces it wherever it applies, 0
+  // turns it off. Measured, K 4096, N 14336: fp8 64 rows 21.7 us against
+  // 23.4 (two-launch kernel), 48 rows 21.6 against 22.8; it ties at 24 and
+  // 32 rows (single-launch kernel) and with 16-bit W and gamma (64 rows
+  // 30.3 against 30.5), and loses without gamma to the raw-x form (bf16 W,
+  // 48 rows: 30.0 against 27.1).
+  if (aligned && (!gamma || gt == MTP_F32) && tune(kTuneSkw) != 0) {
+    bool want = tune(kTuneSkw) == 1;
+    if (!want && gamma && M > 32 && tune(kTuneSkl) != 1 && tune(kTuneSkSplits) <= 0) {
+      const PlanSk nat = make_plan_sk(xt, wt, M, N, K, true);
+      want = nat.ok && nat.S == 1;
+    }
+    const PlanSk ps = want ? make_plan_sk(xt, wt, M, N, K, gamma != nullptr, true) : PlanSk{};
+    if (ps.ok) {
+      if (!ws || ws_bytes < ps.total) return MTP_ERR_WORKSPACE;
+      SkArgs sa{};
+      sa.w = w;
+      sa.wscale = wscale;
+      sa.bias = bias;
+      sa.bias_dt = bt;
+      sa.y = y;
+      sa.M = (int)M;
+      sa.N = (int)N;
+      sa.K = (int)K;
+      sa.scale = scale;
+      return launch_sk(ps, x, (const float *)gamma, eps, norm, sa, ws, st);
     }
   }
   const int sklm = skl_mode();
@@ -1137,6 +1196,8 @@ size_t mtp_rmsnorm_linear_workspace_bytes(int x_dtype, int w_kind, int64_t M, in
     if (p.ok && p.total > most) most = p.total;
     PlanSk q = make_plan_sk(x_dtype, w_kind, M, N, K, gam != 0);
     if (q.ok && q.total > most) most = q.total;
+    PlanSk qw = make_plan_sk(x_dtype, w_kind, M, N, K, gam != 0, true);
+    if (qw.ok && qw.total > most) most = qw.total;
     PlanSkl l = make_plan_skl(x_dtype, w_kind, M, N, K, gam != 0);
     if (l.ok && l.total > most) most = l.total;
     PlanSkp q2 = make_plan_skp(x_dtype, w_kind, M, N, K, gam != 0);

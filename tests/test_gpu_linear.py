@@ -210,6 +210,52 @@ def test_skinny_kernel_splits(splits, M, N, K, wkind, xdtype):
                                ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5))
 
 
+SKW_SHAPES = [(17, 300, 512), (33, 260, 1024), (64, 1000, 2048), (40, 100, 128),
+              (64, 64, 256), (24, 520, 768), (57, 130, 8192), (32, 4100, 384)]
+
+
+@pytest.mark.parametrize("M,N,K", SKW_SHAPES)
+@pytest.mark.parametrize("wkind", ["fp8", "same"])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+def test_wave_specialised_skinny_kernel(M, N, K, wkind, xdtype):
+    """The wave-specialised skinny kernel after the prep launch (forced with
+    the tuning key skw=1): ragged M (one or two 32-row tiles) and N, K from
+    one stage (128 fp8 / 64 16-bit k, fewer stages than its ring) to 8192;
+    with gamma, norm and bias, without norm, and without gamma, against the
+    oracle, and bit for bit on a second call."""
+    _set(skw=1)
+    from mtp_hip import ops
+    print(f"case skw M={M} N={N} K={K} w={wkind} x={xdtype}", flush=True)
+    g = torch.Generator().manual_seed(M * 977 + N + K)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(xdtype)
+    if wkind == "fp8":
+        if K % 128:
+            pytest.skip("fp8 stages are 128 k")
+        wq, ws = O.quantize_fp8_per_channel(W)
+        run = lambda **kw: ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), kw.get("b"), 1e-6,
+                                                  gamma=kw.get("gm"), norm=kw.get("norm", True))
+        oracle = lambda **kw: O.rmsnorm_linear_fp8(x, wq, ws, kw.get("b"), 1e-6,
+                                                   gamma=kw.get("gm"), norm=kw.get("norm", True))
+    else:
+        Wc = W.to(xdtype)
+        run = lambda **kw: ops.rmsnorm_linear(_dev(x), _dev(Wc), kw.get("b"), 1e-6, 0.5,
+                                              gamma=kw.get("gm"), norm=kw.get("norm", True))
+        oracle = lambda **kw: O.rmsnorm_linear(x, Wc, kw.get("b"), 1e-6, 0.5,
+                                               gamma=kw.get("gm"), norm=kw.get("norm", True))
+    cases = [dict(gm=gm, b=b), dict(norm=False), dict(b=b)]
+    for kw in cases:
+        dev_kw = {k: (_dev(v) if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+        y = run(**dev_kw)
+        ref = oracle(**kw)
+        torch.cuda.synchronize()
+        ok, worst = close(y, ref, 2e-2)
+        assert ok, f"{sorted(kw)}: worst err/bound = {worst:.3g}"
+        assert torch.equal(y, run(**dev_kw))  # fixed order: bit for bit
+
+
 SKL_CASES = [(None, "8", (40, 40000, 512)), (None, "8", (3, 33024, 256)),
              ("1", "4", (64, 1000, 2048)), ("1", "8", (7, 300, 512)),
              ("2", "8", (33, 260, 1024)), ("3", "4", (1, 128, 1280)),
