@@ -1,6 +1,8 @@
 """HIP-graph capture of the hot path: a draft step (RMSNorm, RMSNorm ->
 linear head, greedy token + embedding, combine-norm), the fp32 linear
-routes (one launch, streaming, row-chunk with K-splits), the persistent multi-verify and the device-side
+routes (one launch, streaming, row-chunk with K-splits), the fp8 skinny
+routes (prep + wave-specialised GEMM, prep + split-K GEMM, single launch),
+the persistent multi-verify and the device-side
 commit are each captured once on a warmed-up stream and replayed with new
 input contents; every replay equals the eager result bit for bit (the
 kernels re-arm their tickets and keys themselves), with eager work and
@@ -88,6 +90,33 @@ def test_fp32_linear_graph_replay(route):
         _replays(graph, out, lambda i: x.copy_(xs[i]), fn)
     finally:
         L.set_tuning(sf32=-1)
+
+
+@pytest.mark.parametrize("M,N,keys", [(64, 14336, {}), (48, 4096, {}), (32, 14336, {}),
+                                      (64, 4096, {"sk_splits": 3})])
+def test_fp8_linear_graph_replay(M, N, keys):
+    """The fp8 RMSNorm -> linear routes under capture at K = 4096 with gamma:
+    the prep launch + wave-specialised GEMM (64 rows x 14336), the
+    two-launch GEMM with planned and forced K-splits (48 / 64 rows x 4096:
+    split tickets re-armed on every replay) and the single-launch kernel
+    (32 rows x 14336)."""
+    from mtp_hip import _lib as L, ops, workloads
+    d = workloads.fp8_linear(M)
+    K = d["x"].shape[1]
+    g = torch.Generator().manual_seed(M + N)
+    wq = d["weight_fp8"][:N].to(DEV)
+    ws = d["wscale"][:N].to(DEV)
+    x = d["x"].to(DEV)
+    gm = d["gamma"].to(DEV)
+    print(f"case fp8 graph M={M} N={N} K={K} keys={keys}", flush=True)
+    L.set_tuning(**keys)
+    try:
+        fn = lambda: ops.rmsnorm_linear_fp8(x, wq, ws, None, d["eps"], gamma=gm)  # noqa: E731
+        graph, out = _capture(fn)
+        xs = [torch.randn(x.shape, generator=g).to(x.dtype).to(DEV) for _ in range(4)]
+        _replays(graph, out, lambda i: x.copy_(xs[i]), fn)
+    finally:
+        L.set_tuning(**{k: -1 for k in keys})
 
 
 @pytest.mark.parametrize("dtype,bias", [(torch.bfloat16, None), (torch.bfloat16, torch.bfloat16),
