@@ -2,6 +2,7 @@
 linear head, greedy token + embedding, combine-norm), the fp32 linear
 routes (one launch, streaming, row-chunk with K-splits), the fp8 skinny
 routes (prep + wave-specialised GEMM, prep + split-K GEMM, single launch),
+the tree-verify attention (chunk launch + merge launch),
 the persistent multi-verify and the device-side
 commit are each captured once on a warmed-up stream and replayed with new
 input contents; every replay equals the eager result bit for bit (the
@@ -117,6 +118,34 @@ def test_fp8_linear_graph_replay(M, N, keys):
         _replays(graph, out, lambda i: x.copy_(xs[i]), fn)
     finally:
         L.set_tuning(**{k: -1 for k in keys})
+
+
+def test_tree_verify_attention_graph_replay():
+    """The tree-verify attention (64 nodes, 4 heads, 700 paged context keys
+    and the tree keys in one-block chunks: 12 chunks per head) under capture:
+    the chunk launch and the merge launch replay with new queries."""
+    from mtp_hip import _lib as L, ops, workloads
+    g = torch.Generator().manual_seed(7)
+    N, H, D, Lc, ps = 64, 4, 128, 700, 16
+    dt = torch.bfloat16
+    npg = (Lc + ps - 1) // ps
+    tm = workloads.draft_tree_mask(16, 4)[:N, :N].to(DEV)
+    q = torch.randn(N, H, D, generator=g).to(dt).to(DEV)
+    kt = torch.randn(N, H, D, generator=g).to(dt).to(DEV)
+    vt = torch.randn(N, H, D, generator=g).to(dt).to(DEV)
+    kp = torch.randn(npg + 2, 1, H, ps, D, generator=g).to(dt).to(DEV)
+    vp = torch.randn(npg + 2, 1, H, ps, D, generator=g).to(dt).to(DEV)
+    table = torch.randperm(npg + 2, generator=g)[:npg].repeat_interleave(ps)[:Lc]
+    table = table.to(torch.int32)[None, :].to(DEV)
+    print("case tree-verify attention graph", flush=True)
+    L.set_tuning(attn_chunk_blocks=1)
+    try:
+        fn = lambda: ops.tree_verify_attention(q, kp, vp, table, ps, kt, vt, tm)  # noqa: E731
+        graph, out = _capture(fn)
+        qs = [torch.randn(q.shape, generator=g).to(dt).to(DEV) for _ in range(4)]
+        _replays(graph, out, lambda i: q.copy_(qs[i]), fn)
+    finally:
+        L.set_tuning(attn_chunk_blocks=-1)
 
 
 @pytest.mark.parametrize("dtype,bias", [(torch.bfloat16, None), (torch.bfloat16, torch.bfloat16),
