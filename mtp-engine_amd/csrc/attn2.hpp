@@ -8,8 +8,8 @@
 // (queries 32 qg .. + 31) and key group kg = w >> 1 (keys 32 kg .. + 31 of
 // every step), so every K row and V row is read from LDS by two waves
 // (16-query tiles need four).
-//   * K and V rows go HBM -> LDS by buffer loads with the LDS bit (no
-//     registers, no VALU): one instruction fills 1 KB = 4 rows of 256 B,
+//   * K and V rows go HBM -> LDS by non-temporal buffer loads with the LDS
+//     bit (no registers, no VALU): one instruction fills 1 KB = 4 rows of 256 B,
 //     lane i the 16-byte position i % 16 of row i / 16, which holds the
 //     row's chunk (i % 16) ^ swz(row). Two step buffers (64 KB each): step
 //     s + 1 lands while step s is multiplied. Keys that are missing (past
