@@ -58,6 +58,7 @@ enum TuneKey {
   kTuneAttn32,           // MTP_ATTN32: 32-query-tile attention (33 .. 64 queries, D 128), 0 off
   kTuneSkXraw,           // MTP_SK_XRAW: 0 keeps sk's prep launch without gamma (default: raw x)
   kTuneSkw,              // MTP_SKW: wave-specialised skinny kernel, 1 force where it applies, 0 off
+  kTuneSkwTw,            // MTP_SKW_TW: its output columns per workgroup (8 .. 64, multiple of 8)
   kTuneCount
 };
 int tune(TuneKey k);

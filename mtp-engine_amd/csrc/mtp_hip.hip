@@ -32,7 +32,7 @@ std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
     "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw",
-    "skw"};
+    "skw", "skw_tw"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -67,6 +67,7 @@ void tune_init() {
   g_tune[kTuneAttn32].store(env_int("MTP_ATTN32", -1), std::memory_order_relaxed);
   g_tune[kTuneSkXraw].store(env_int("MTP_SK_XRAW", -1), std::memory_order_relaxed);
   g_tune[kTuneSkw].store(env_int("MTP_SKW", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkwTw].store(env_int("MTP_SKW_TW", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -378,6 +379,7 @@ struct PlanSk {
   int ct = 0, wt = 0, mt = 0;
   bool gam = false, xr = false, skw = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
+  int tw = kSkBN;       // output columns per workgroup (the wave-specialised GEMM may take fewer)
   int ch = 1, nsl = 0;  // prep form: 256 ch k per prep slice, slices
   size_t xf_off = 0, pss_off = 0, part_off = 0, ss_off = 0, total = 0;
 };
@@ -416,7 +418,23 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam,
   // against 16.3 with the prep; bf16 32 x 4096 x 4096: 12.0 against 14.5;
   // fp8 64 x 14336 x 4096: 25.1 either way)
   p.xr = !gam && tune(kTuneSkXraw) != 0 && !skw;
-  p.G = (int)((N + kSkBN - 1) / kSkBN);
+  if (skw) {
+    // the wave-specialised GEMM spreads the columns over every CU: the
+    // smallest multiple of 8 that needs at most one workgroup per CU (its
+    // MFMA tile stays 64 wide). fp8 64 x 14336 x 4096: 56 columns, 256
+    // workgroups, 21.15 us against 21.64 with 64 columns (224 workgroups);
+    // bf16 28.0 against 30.2. Tuning key skw_tw sets the width.
+    const int t = tune(kTuneSkwTw);
+    if (t > 0) {
+      if (t > kSkBN || t % 8 != 0) return p;
+      p.tw = t;
+    } else {
+      const int64_t cus = device_cus();
+      const int64_t per = (N + cus - 1) / cus;
+      p.tw = (int)std::min<int64_t>(kSkBN, std::max<int64_t>(8, (per + 7) / 8 * 8));
+    }
+  }
+  p.G = (int)((N + p.tw - 1) / p.tw);
   p.nkb = (int)(K * wb / kSkUB);
   int S = 1;
   if (skw) {
@@ -510,6 +528,7 @@ int launch_sk(const PlanSk &p, const void *x, const float *gamma, float eps, int
     wa.K = a.K;
     wa.scale = a.scale;
     wa.nst = p.nkb;
+    wa.tw = p.tw;
     hipLaunchKernelGGL(kw, dim3((unsigned)p.G), dim3(512), 0, st, wa);
     return launch_status();
   }

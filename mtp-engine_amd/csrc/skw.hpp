@@ -67,7 +67,11 @@ skw_kernel(const SkwArgs a) {
 
   const int th = threadIdx.x, lane = th & 63, wave = th >> 6;
   const int N = a.N, K = a.K, nst = a.nst;
-  const int tile = (int)blockIdx.x, n0 = tile * kSkBN;
+  // tw <= 64 output columns per workgroup; the MFMA tile stays 64 wide
+  // (rows past the workgroup's columns read zeros and are not stored)
+  const int tw = a.tw;
+  const int tile = (int)blockIdx.x, n0 = tile * tw;
+  const int nend = min(N, n0 + tw);
   const int rot = (7 * tile) % nst;
   auto k_stage = [&](int s) {
     const int r = s + rot;
@@ -91,7 +95,7 @@ skw_kernel(const SkwArgs a) {
   if (wave < 4) {
     load_col_factors<4>(a.wscale, a.bias, a.bias_dt, N, n0 + 32 * ou + 4 * ag, 8, cws, cbi);
     const uint32_t ldw = (uint32_t)K * (FP8 ? 1u : 2u);
-    const int nrows = min(kSkBN, N - n0);  // rows past N read zeros
+    const int nrows = nend - n0;  // rows past the workgroup's columns read zeros
     const __amdgpu_buffer_rsrc_t wrs =
         make_rsrc((const unsigned char *)a.w + (int64_t)n0 * ldw, (uint32_t)nrows * ldw);
     const __amdgpu_buffer_rsrc_t nrs = make_rsrc(a.w, 0u);
@@ -241,20 +245,21 @@ skw_kernel(const SkwArgs a) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int n = n0 + 32 * ou + 8 * g + 4 * ag;
+    if (n >= nend) continue;
     float o[4];
 #pragma unroll
     for (int jx = 0; jx < 4; ++jx)
       o[jx] = (a.bias ? v[4 * g + jx] * cws[4 * g + jx] + cbi[4 * g + jx]
                       : v[4 * g + jx] * cws[4 * g + jx]) * a.scale;
     const int64_t yb = (int64_t)m * N + n;
-    if (n + 3 < N && (N & 3) == 0) {
+    if (n + 3 < nend && (N & 3) == 0) {
       uint2 pk;
       pk.x = pack2<CT>(o[0], o[1]);
       pk.y = pack2<CT>(o[2], o[3]);
       *(uint2 *)((uint16_t *)a.y + yb) = pk;
     } else {
       for (int jx = 0; jx < 4; ++jx)
-        if (n + jx < N) store_from_f32(a.y, CT, yb + jx, o[jx]);
+        if (n + jx < nend) store_from_f32(a.y, CT, yb + jx, o[jx]);
     }
   }
 }

@@ -22,6 +22,7 @@ struct SkwArgs {
   int M, N, K;
   float scale;
   int nst;              // stages: 128 bytes of every W row each
+  int tw;               // output columns per workgroup (8 .. 64, a multiple of 4)
 };
 
 typedef void (*SkwKernel)(SkwArgs);

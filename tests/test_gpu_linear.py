@@ -256,6 +256,38 @@ def test_wave_specialised_skinny_kernel(M, N, K, wkind, xdtype):
         assert torch.equal(y, run(**dev_kw))  # fixed order: bit for bit
 
 
+@pytest.mark.parametrize("tw", [56, 40, 8])
+@pytest.mark.parametrize("M,N,K,wkind", [(64, 1000, 1024, "fp8"), (33, 260, 384, "same"),
+                                         (48, 4100, 2048, "fp8"), (17, 57, 128, "fp8")])
+def test_wave_specialised_column_widths(M, N, K, wkind, tw):
+    """The wave-specialised kernel with fewer output columns per workgroup
+    than its 64-wide MFMA tile (tuning key skw_tw): the tile's last columns
+    read zeros and are not stored, N ragged against the width; gamma, norm
+    and bias, against the oracle and bit for bit on a second call."""
+    _set(skw=1, skw_tw=tw)
+    from mtp_hip import ops
+    print(f"case skw tw={tw} M={M} N={N} K={K} w={wkind}", flush=True)
+    g = torch.Generator().manual_seed(M * 31 + N + K + tw)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
+        again = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+    else:
+        Wc = W.to(torch.bfloat16)
+        y = ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        again = ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5, gamma=gm)
+    torch.cuda.synchronize()
+    ok, worst = close(y, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+    assert torch.equal(y, again)
+
+
 SKL_CASES = [(None, "8", (40, 40000, 512)), (None, "8", (3, 33024, 256)),
              ("1", "4", (64, 1000, 2048)), ("1", "8", (7, 300, 512)),
              ("2", "8", (33, 260, 1024)), ("3", "4", (1, 128, 1280)),
