@@ -86,13 +86,15 @@ const char *mtp_last_hip_error(void);
  * kernel for at most 8 rows), "sf32" (0: no one-launch fp32 kernels for at most 32 rows), "attn32"
  * (0: 16-query-tile attention for 33 .. 64 queries), "sk_xraw" (0: the
  * skinny kernel keeps its prep launch without gamma too), "skw" (1: the
- * wave-specialised skinny GEMM wherever it applies, 0: never), "skw_tw"
- * (its output columns per workgroup, a multiple of 8 up to 64; default: the
- * smallest that needs at most one workgroup per CU). value -1
+ * wave-specialised skinny GEMM wherever it applies, 0: never), "skw_tw",
+ * "skp_tw", "skl_tw" (output columns per workgroup of the wave-specialised,
+ * x-resident and single-launch skinny kernels, a multiple of 8 up to their
+ * tile width; default: narrowed by at most a quarter so that the grid puts
+ * one workgroup on every CU). value -1
  * restores the planner's choice. The MTP_SKL, MTP_SK_SPLITS, MTP_WS_TUNE
  * ("variant,splits"), MTP_SKL_WAVES, MTP_SKL_SPLITS, MTP_ATTN_CHUNK_BLOCKS,
  * MTP_INT4_WAVES, MTP_VERIFY_WSTREAM, MTP_SKP, MTP_SKP_SPLITS, MTP_SKP_TA,
- * MTP_SKP_H8, MTP_SF32, MTP_ATTN32, MTP_SK_XRAW, MTP_SKW and MTP_SKW_TW environment variables
+ * MTP_SKP_H8, MTP_SF32, MTP_ATTN32, MTP_SK_XRAW, MTP_SKW, MTP_SKW_TW, MTP_SKP_TW and MTP_SKL_TW environment variables
  * seed the keys once, at the
  * first launch plan. MTP_ERR_ARG for an unknown key.
  */

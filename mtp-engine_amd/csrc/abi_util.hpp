@@ -59,6 +59,8 @@ enum TuneKey {
   kTuneSkXraw,           // MTP_SK_XRAW: 0 keeps sk's prep launch without gamma (default: raw x)
   kTuneSkw,              // MTP_SKW: wave-specialised skinny kernel, 1 force where it applies, 0 off
   kTuneSkwTw,            // MTP_SKW_TW: its output columns per workgroup (8 .. 64, multiple of 8)
+  kTuneSkpTw,            // MTP_SKP_TW: x-resident kernel's columns per workgroup (multiple of 8)
+  kTuneSklTw,            // MTP_SKL_TW: single-launch kernel's columns per workgroup (multiple of 8)
   kTuneCount
 };
 int tune(TuneKey k);

@@ -32,7 +32,7 @@ std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
     "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw",
-    "skw", "skw_tw"};
+    "skw", "skw_tw", "skp_tw", "skl_tw"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -68,6 +68,8 @@ void tune_init() {
   g_tune[kTuneSkXraw].store(env_int("MTP_SK_XRAW", -1), std::memory_order_relaxed);
   g_tune[kTuneSkw].store(env_int("MTP_SKW", -1), std::memory_order_relaxed);
   g_tune[kTuneSkwTw].store(env_int("MTP_SKW_TW", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkpTw].store(env_int("MTP_SKP_TW", -1), std::memory_order_relaxed);
+  g_tune[kTuneSklTw].store(env_int("MTP_SKL_TW", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -386,6 +388,17 @@ struct PlanSk {
 
 // aim for most of the CUs busy (200 of 256)
 int sk_min_blocks() { return device_cus() * 200 / 256; }
+// Columns per workgroup for a kernel whose natural tile is `full` columns
+// (S K-splits each): the multiple of 8 that puts at most one workgroup on
+// every CU, when that narrows the tile by at most a quarter (the grid
+// already covers most of the CUs; narrower tiles would multiply the x
+// bytes per output column), else `full`.
+int fill_width(int64_t N, int S, int full) {
+  const int64_t cus = device_cus();
+  const int64_t per = (N * S + cus - 1) / cus;
+  const int64_t w = (per + 7) / 8 * 8;
+  return (w < full && 4 * w >= 3 * (int64_t)full) ? (int)w : full;
+}
 constexpr int kSkMinStages = 4;    // stages per split at least
 
 // Tile: 64 columns x all rows of x (<= 64); K-splits only while the grid is
@@ -419,19 +432,17 @@ PlanSk make_plan_sk(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam,
   // fp8 64 x 14336 x 4096: 25.1 either way)
   p.xr = !gam && tune(kTuneSkXraw) != 0 && !skw;
   if (skw) {
-    // the wave-specialised GEMM spreads the columns over every CU: the
-    // smallest multiple of 8 that needs at most one workgroup per CU (its
-    // MFMA tile stays 64 wide). fp8 64 x 14336 x 4096: 56 columns, 256
-    // workgroups, 21.15 us against 21.64 with 64 columns (224 workgroups);
-    // bf16 28.0 against 30.2. Tuning key skw_tw sets the width.
+    // the wave-specialised GEMM spreads the columns over every CU when the
+    // 64-column grid leaves a few idle (its MFMA tile stays 64 wide). fp8
+    // 64 x 14336 x 4096: 56 columns, 256 workgroups, 21.15 us against 21.64
+    // with 64 columns (224 workgroups); bf16 28.0 against 30.2. Tuning key
+    // skw_tw sets the width.
     const int t = tune(kTuneSkwTw);
     if (t > 0) {
       if (t > kSkBN || t % 8 != 0) return p;
       p.tw = t;
     } else {
-      const int64_t cus = device_cus();
-      const int64_t per = (N + cus - 1) / cus;
-      p.tw = (int)std::min<int64_t>(kSkBN, std::max<int64_t>(8, (per + 7) / 8 * 8));
+      p.tw = fill_width(N, 1, kSkBN);
     }
   }
   p.G = (int)((N + p.tw - 1) / p.tw);
@@ -554,6 +565,7 @@ struct PlanSkl {
   int ct = 0, wt = 0, mt = 0, nw = 8;
   bool gam = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
+  int tw = 256;  // output columns per workgroup (<= 32 nw)
   size_t part_off = 0, ss_off = 0, total = 0;
 };
 
@@ -600,6 +612,18 @@ PlanSkl make_plan_skl(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
   }
   if (gam && (int64_t)p.kb_per * uk > kSklGammaMax) return p;
   p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  // columns per workgroup: the tile narrowed to fill every CU (fp8 32 x
+  // 14336 x 4096, 4 splits: 224 columns, 256 workgroups); tuning key
+  // skl_tw sets it
+  p.tw = (int)bn;
+  if (tune(kTuneSklTw) > 0) {
+    const int t = tune(kTuneSklTw);
+    if (t > bn || t % 8 != 0) return p;
+    p.tw = t;
+  } else {
+    p.tw = fill_width(N, p.S, (int)bn);
+  }
+  p.G = (int)((N + p.tw - 1) / p.tw);
   if ((int64_t)p.G * p.S > INT32_MAX) return p;
   if (p.S > 1 && p.G > kCounterSlots) return p;
   size_t off = kCounterBytes;
@@ -624,6 +648,7 @@ int launch_skl(const PlanSkl &p, SklArgs &a, void *ws, hipStream_t st) {
   a.S = p.S;
   a.kb_per = p.kb_per;
   a.nkb = p.nkb;
+  a.tw = p.tw;
   // the splits of a tile on one XCD from 4 splits up (fp8 24 x 14336 x
   // 4096: 19.1 -> 17.6 us); with 2 splits it loses (fp8 64 x 28672 x 4096:
   // 38.4 -> 39.9 us)
@@ -649,6 +674,7 @@ struct PlanSkp {
   int ct = 0, wt = 0, mt = 0, ta = 1;
   bool gam = false, h8 = false;
   int G = 0, S = 1, kb_per = 0, nkb = 0;
+  int tw = 64;  // output columns per workgroup (<= 64 ta)
   size_t lds = 0, part_off = 0, ss_off = 0, total = 0;
 };
 
@@ -711,7 +737,17 @@ PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
         break;
       }
   }
-  p.G = (int)((N + 64 * p.ta - 1) / (64 * p.ta));
+  // columns per workgroup: the tile narrowed to fill every CU (fp8 8 x
+  // 14336 x 4096: 56 columns, 256 workgroups); tuning key skp_tw sets it
+  p.tw = 64 * p.ta;
+  if (tune(kTuneSkpTw) > 0) {
+    const int t = tune(kTuneSkpTw);
+    if (t > 64 * p.ta || t % 8 != 0) return p;
+    p.tw = t;
+  } else {
+    p.tw = fill_width(N, p.S, 64 * p.ta);
+  }
+  p.G = (int)((N + p.tw - 1) / p.tw);
   if ((int64_t)p.G * p.S > INT32_MAX) return p;
   if (p.S > 1 && p.G > kCounterSlots) return p;
   p.lds = skp_lds_bytes(p.mt, xp, p.kb_per, uk, gam);
@@ -738,6 +774,7 @@ int launch_skp(const PlanSkp &p, SkpArgs &a, void *ws, hipStream_t st) {
   a.S = p.S;
   a.kb_per = p.kb_per;
   a.nkb = p.nkb;
+  a.tw = p.tw;
   // the splits of a tile on one XCD with compact x blocks (fp8 8 x 4096 x
   // 4096: 10.3 -> 9.5 us); with full blocks it loses (bf16 16 x 4096 x
   // 4096: 11.1 -> 11.4 us)

@@ -83,7 +83,10 @@ skl_kernel(const SklArgs a) {
   const int b = blockIdx.x;
   int tile, sp;
   split_tile_of(b, a.G, a.S, a.xg != 0, tile, sp);
-  const int n0 = tile * BN;
+  // tw <= BN output columns; the tile's rows past them read zeros and are
+  // not stored
+  const int n0 = tile * a.tw;
+  const int nend = min(N, n0 + a.tw);
   const int st0 = sp * a.kb_per;
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // stages of this split (>= 1)
   const int rot = (7 * b) % nst;
@@ -97,7 +100,7 @@ skl_kernel(const SklArgs a) {
   // W load c (c = wave + NW i): rows 8 c .. 8 c + 7 of the tile, lane l: row
   // 8 c + l / 8, 16-byte chunk (l % 8) ^ sk_swz(row) of the stage's 128 bytes
   const uint32_t ldw = (uint32_t)K * (FP8 ? 1u : 2u);
-  const int nrows = min(BN, N - n0);
+  const int nrows = nend - n0;
   const __amdgpu_buffer_rsrc_t wrs =
       make_rsrc((const unsigned char *)a.w + (int64_t)n0 * ldw, (uint32_t)nrows * ldw);
   uint32_t wvo[NWC];
@@ -303,21 +306,21 @@ skl_kernel(const SklArgs a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int n = n0 + 32 * wave + 8 * g + 4 * ag;
-        if (n >= N) continue;
+        if (n >= nend) continue;
         float o[4];
 #pragma unroll
         for (int jx = 0; jx < 4; ++jx)
           o[jx] = (a.bias ? r[t][4 * g + jx] * rs * cws[4 * g + jx] + cbi[4 * g + jx]
                           : r[t][4 * g + jx] * rs * cws[4 * g + jx]) * a.scale;
         const int64_t yb = (int64_t)m * N + n;
-        if (n + 3 < N && (N & 3) == 0) {
+        if (n + 3 < nend && (N & 3) == 0) {
           uint2 pk;
           pk.x = pack2<CT>(o[0], o[1]);
           pk.y = pack2<CT>(o[2], o[3]);
           *(uint2 *)((uint16_t *)a.y + yb) = pk;
         } else {
           for (int jx = 0; jx < 4; ++jx)
-            if (n + jx < N) store_from_f32(a.y, CT, yb + jx, o[jx]);
+            if (n + jx < nend) store_from_f32(a.y, CT, yb + jx, o[jx]);
         }
       }
     }

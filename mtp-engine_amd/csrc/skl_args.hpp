@@ -21,6 +21,7 @@ struct SklArgs {
   float eps, scale;
   int G, S, kb_per, nkb;  // column tiles, K-splits, stages per split, stages
   int xg;                 // 1: the splits of a tile on one XCD (split_tile_of)
+  int tw;                 // output columns per workgroup (<= 32 waves, a multiple of 4)
   float *part;            // split-K partial tiles [G * S][tile] (S > 1)
   float *part_ss;         // split-K partial sums of squares [G * S][64] (S > 1)
   unsigned *ticket;       // [G] arrival tickets (S > 1)

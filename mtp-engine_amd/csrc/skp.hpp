@@ -98,7 +98,10 @@ skp_kernel(const SkpArgs a) {
   const int b = blockIdx.x;
   int tile, sp;
   split_tile_of(b, a.G, a.S, a.xg != 0, tile, sp);
-  const int n0 = tile * BN;
+  // tw <= BN output columns; the tile's rows past them read zeros and are
+  // not stored
+  const int n0 = tile * a.tw;
+  const int nend = min(N, n0 + a.tw);
   const int st0 = sp * a.kb_per;
   const int nst = min(a.nkb, st0 + a.kb_per) - st0;  // steps of this split (>= 1)
   const int rot = (7 * b) % nst;
@@ -158,7 +161,7 @@ skp_kernel(const SkpArgs a) {
   }
 
   const uint32_t ldw = (uint32_t)K * (FP8 ? 1u : 2u);
-  const int nrows = min(BN, N - n0);
+  const int nrows = nend - n0;
   const __amdgpu_buffer_rsrc_t wrs =
       make_rsrc((const unsigned char *)a.w + (int64_t)n0 * ldw, (uint32_t)nrows * ldw);
   // W load v = 2 i + h of a step: rows 16 (w TA + i) + 8 h + lane / 8 of the
@@ -375,21 +378,21 @@ skp_kernel(const SkpArgs a) {
 #pragma unroll
       for (int i = 0; i < TA; ++i) {
         const int n = n0 + 16 * (TA * wave + i) + 4 * (lane >> 4);
-        if (n >= N) continue;
+        if (n >= nend) continue;
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o[e] = (a.bias ? r[i][t][e] * rs * cws[4 * i + e] + cbi[4 * i + e]
                          : r[i][t][e] * rs * cws[4 * i + e]) * a.scale;
         const int64_t yb = (int64_t)m * N + n;
-        if (n + 3 < N && (N & 3) == 0) {
+        if (n + 3 < nend && (N & 3) == 0) {
           uint2 pk;
           pk.x = pack2<CT>(o[0], o[1]);
           pk.y = pack2<CT>(o[2], o[3]);
           *(uint2 *)((uint16_t *)a.y + yb) = pk;
         } else {
           for (int e = 0; e < 4; ++e)
-            if (n + e < N) store_from_f32(a.y, CT, yb + e, o[e]);
+            if (n + e < nend) store_from_f32(a.y, CT, yb + e, o[e]);
         }
       }
     }

@@ -29,6 +29,7 @@ struct SkpArgs {
   int G, S;             // column tiles, K-splits
   int kb_per, nkb;      // steps per split, steps in K
   int xg;               // 1: the splits of a tile on one XCD (split_tile_of)
+  int tw;               // output columns per workgroup (<= 64 TA, a multiple of 4)
   float *part;          // [G][S][waves][TA][MT][64] f32x4 (S > 1)
   float *part_ss;       // [G][S][64]
   unsigned *ticket;     // [G]

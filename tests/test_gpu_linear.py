@@ -340,6 +340,46 @@ def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
     assert torch.equal(y, y3)
 
 
+# (columns per workgroup, K-splits, waves, (M, N, K), W kind)
+SKL_TW_CASES = [(224, "4", "8", (32, 3000, 2048), "fp8"), (200, None, "8", (24, 1000, 1024), "fp8"),
+                (64, "2", "4", (40, 300, 512), "same"), (8, None, "8", (7, 100, 256), "fp8"),
+                (120, "3", "4", (64, 520, 1536), "fp8")]
+
+
+@pytest.mark.parametrize("tw,splits,waves,shape,wkind", SKL_TW_CASES)
+def test_single_launch_column_widths(tw, splits, waves, shape, wkind):
+    """The single-launch kernel with fewer output columns per workgroup than
+    its 32 x waves-wide tile (tuning key skl_tw): the tile's last columns
+    read zeros and are not stored; with and without K-splits, 4 and 8
+    waves, ragged N; against the oracle and bit for bit on a second call."""
+    M, N, K = shape
+    _set(skl=1, skl_tw=tw, skl_waves=int(waves))
+    if splits is not None:
+        _set(skl_splits=int(splits))
+    from mtp_hip import ops
+    print(f"case skl tw={tw} splits={splits} waves={waves} M={M} N={N} K={K} w={wkind}",
+          flush=True)
+    g = torch.Generator().manual_seed(M * 41 + N + K + tw)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        run = lambda: ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6,
+                                             gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+    else:
+        Wc = W.to(torch.bfloat16)
+        run = lambda: ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5, gamma=gm)
+    y = run()
+    torch.cuda.synchronize()
+    ok, worst = close(y, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+    assert torch.equal(y, run())
+
+
 # (K-splits, A tiles per wave, compact <= 8-row blocks, (M, N, K)); None: planned
 SKP_CASES = [(None, None, None, (1, 64, 128)), (None, None, None, (5, 200, 384)),
              (None, None, None, (16, 300, 4096)),
@@ -402,6 +442,48 @@ def test_x_resident_skinny_kernel(splits, ta, h8, shape, wkind, xdtype):
     for out, r in ((y, ref), (y2, ref2)):
         ok, worst = close(out, r, 2e-2)
         assert ok, f"worst err/bound = {worst:.3g}"
+    assert torch.equal(y, run())
+
+
+# (columns per workgroup, K-splits, A tiles per wave, (M, N, K), W kind)
+SKP_TW_CASES = [(56, None, None, (8, 1000, 4096), "fp8"), (40, "2", None, (5, 300, 1024), "fp8"),
+                (8, None, None, (16, 57, 512), "same"), (112, None, "2", (9, 700, 2048), "fp8"),
+                (48, "3", "1", (33, 260, 1536), "fp8"), (24, None, None, (2, 100, 256), "same")]
+
+
+@pytest.mark.parametrize("tw,splits,ta,shape,wkind", SKP_TW_CASES)
+def test_x_resident_column_widths(tw, splits, ta, shape, wkind):
+    """The x-resident kernel with fewer output columns per workgroup than
+    its 64 TA-wide tile (tuning key skp_tw): the tile's last columns read
+    zeros and are not stored; with and without K-splits, one or two A tiles
+    per wave, ragged N; against the oracle and bit for bit on a second
+    call."""
+    M, N, K = shape
+    _set(skp=1, skp_tw=tw)
+    if splits is not None:
+        _set(skp_splits=int(splits))
+    if ta is not None:
+        _set(skp_ta=int(ta))
+    from mtp_hip import ops
+    print(f"case skp tw={tw} splits={splits} ta={ta} M={M} N={N} K={K} w={wkind}", flush=True)
+    g = torch.Generator().manual_seed(M * 37 + N + K + tw)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = 0.05 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    if wkind == "fp8":
+        wq, ws = O.quantize_fp8_per_channel(W)
+        run = lambda: ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6,
+                                             gamma=_dev(gm))
+        ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+    else:
+        Wc = W.to(torch.bfloat16)
+        run = lambda: ops.rmsnorm_linear(_dev(x), _dev(Wc), _dev(b), 1e-6, 0.5, gamma=_dev(gm))
+        ref = O.rmsnorm_linear(x, Wc, b, 1e-6, 0.5, gamma=gm)
+    y = run()
+    torch.cuda.synchronize()
+    ok, worst = close(y, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
     assert torch.equal(y, run())
 
 
