@@ -12,7 +12,9 @@
 // which every workgroup reads for its columns: per W byte, 2 M / (32 NW)
 // bytes for fp8 W (NW waves, 32 columns each), so the workgroups are made
 // wide (256 columns at NW = 8) and the K range is split among workgroups
-// (split-K) until the grid covers the CUs.
+// (split-K) until the grid covers the CUs; the host then narrows the
+// workgroup's columns (tw, by at most a quarter) to put one workgroup on
+// every CU, the tile's rows past them reading zeros.
 //
 // Workgroup = NW waves, tile of 32 NW columns x all rows, a range of stages.
 // A stage is 128 bytes of every W row of the tile (128 k for fp8, 64 k for

@@ -13,7 +13,9 @@
 // that way and narrows the column tile so the grid still covers the CUs),
 // and after that streams only W.
 //
-// Workgroup = 4 waves (one per SIMD) and a tile of 64 TA columns; wave w
+// Workgroup = 4 waves (one per SIMD) and a tile of 64 TA columns, of which
+// the first tw are the workgroup's (the host narrows the tile by at most a
+// quarter to put one workgroup on every CU; rows past tw read zeros); wave w
 // owns A tiles (16 columns each) w TA .. w TA + TA - 1 against all rows,
 // over every k of the split, so the waves never wait for each other in the
 // main loop. A step is 128 bytes of every W row (128 k for fp8, 64 for

@@ -1,6 +1,8 @@
 // Wave-specialised skinny GEMM for gfx950: the RMSNorm -> linear product of
-// sk.hpp (at most 64 rows of 16-bit x, fp8-e4m3 or 16-bit W, a 64-column
-// tile of the output per workgroup over all of K), after sk.hpp's prep
+// sk.hpp (at most 64 rows of 16-bit x, fp8-e4m3 or 16-bit W, tw <= 64
+// output columns per workgroup over all of K, on a 64-wide MFMA tile whose
+// rows past tw read zeros; the host picks tw to put one workgroup on every
+// CU), after sk.hpp's prep
 // launch (xg = x * gamma rounded to the type of x, written as MFMA B-operand
 // blocks, and each row's sums of squares per K-slice):
 //
