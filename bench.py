@@ -11,7 +11,8 @@ preallocated outputs on torch's current stream, timed with HIP events on
 that stream. Every other workload is timed in the same run into "detail"
 (fp8 at M = 8 / 32, the fp32 TF32-off linear, the multi-verify chain
 without and with the lm_head bias and in fp32 with the bias, the
-tree-verify step, the INT4 linear at M = 256), each with its roofline
+tree-verify step, one draft step of 8 sequences over a 128256-token
+vocabulary, the INT4 linear at M = 256), each with its roofline
 fraction against its own bound; "verify_step_us" holds the verify steps.
 
 Prints ONE JSON line. The CPU baselines time the oracle's eager
@@ -305,6 +306,40 @@ def make_tree_verify_case(torch, lib, L):
     return case
 
 
+def make_draft_step_case(torch, lib, L, B=8, K=4096, V=128256):
+    """One on-device draft step of B sequences (the draft chain around the
+    head GEMM, mtp_engine.py:735-777): RMSNorm of the hidden rows, RMSNorm ->
+    linear onto the vocabulary (bf16 head [V, K] with bias), greedy argmax
+    with the embedding gather of the chosen tokens, and the combine-norm of
+    the normed hidden plus the embeddings (add + RMSNorm). Bound by reading
+    the head weights once."""
+    from mtp_hip import ops
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(11)  # seeded on the device: 2 x 1 GB of draws
+    dt = torch.bfloat16
+    hidden = torch.randn(B, K, generator=g, device=dev).to(dt)
+    nrot = rotations(V * K * 2)
+    wl = [(0.02 * torch.randn(V, K, generator=g, device=dev)).to(dt)]
+    wl += [wl[0].clone() for _ in range(nrot - 1)]
+    bias = (0.1 * torch.randn(V, generator=g, device=dev)).to(dt)
+    head_w = (1 + 0.1 * torch.randn(K, generator=g, device=dev)).to(dt)
+    comb_w = (1 + 0.1 * torch.randn(K, generator=g, device=dev)).to(dt)
+    table = torch.randn(V, K, generator=g, device=dev).to(dt)
+
+    def launch(i):
+        h_norm = ops.rmsnorm(hidden, head_w, 1e-6)
+        logits = ops.rmsnorm_linear(hidden, wl[i % nrot], bias, 1e-6)
+        _, emb = ops.argmax(logits, table)
+        ops.rmsnorm(h_norm, comb_w, 1e-6, residual=emb)
+
+    # head weights and bias once, the logits written and read back, the
+    # hidden rows (three reads), the gathered embeddings, two outputs
+    nbytes = V * K * 2 + V * 2 + 2 * B * V * 2 + 7 * B * K * 2 + 2 * K * 2
+    case = Case(f"draft_step_B{B}_K{K}_V{V}", launch, nbytes, 2 * B * V * K, "hbm", nrot)
+    case.keep = (hidden, wl, bias, head_w, comb_w, table)
+    return case
+
+
 def pmc_traffic(name: str):
     """HBM bytes per launch of the headline kernel from the committed rocprofv3
     --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
@@ -410,6 +445,7 @@ def main():
                 ("multi_verify_fp32", lambda: make_verify_case(torch, lib, L, torch.float32,
                                                                bias=True)),
                 ("tree_verify", lambda: make_tree_verify_case(torch, lib, L)),
+                ("draft_step", lambda: make_draft_step_case(torch, lib, L)),
                 ("int4_M256", lambda: make_int4_case(torch, lib, L))]
     if args.only:
         builders = [b for b in builders if b[0] in args.only.split(",")]

@@ -111,6 +111,35 @@ def test_argmax_strided_rows_and_1d():
     assert int(one) == int(big[2].argmax())
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_argmax_partial_last_chunk(dtype):
+    """Row stride a whole number of 16-byte chunks but V not (the last
+    elements of each row read one at a time): the maximum placed in the
+    partial chunk, tied with an earlier column, NaN there, and a maximum
+    just before it; tokens bit-exact against torch.argmax, with the
+    embedding gather."""
+    from mtp_hip import ops
+    g = torch.Generator().manual_seed(17)
+    big = torch.randn(6, 4096, generator=g).to(dtype)
+    V = 4093  # 4093 % 8 == 5 and 4093 % 4 == 1
+    big[0, 4092] = 50.0                       # maximum in the partial chunk
+    big[1, 4090] = 40.0
+    big[1, 100] = 40.0                        # tie: the lower index wins
+    big[2, 4091] = float("nan")               # NaN in the partial chunk
+    big[3, 4087] = 30.0                       # last column of the last full chunk
+    big[4, 4088] = 30.0                       # first column of the partial chunk
+    big[5, 4095] = 99.0                       # past V: never chosen
+    view = big.to(DEV)[:, :V]
+    table = torch.randn(V, 64, generator=g).to(dtype)
+    tok, emb = ops.argmax(view, table.to(DEV))
+    torch.cuda.synchronize()
+    ref = big[:, :V].float().argmax(-1)
+    ref[2] = 4091
+    assert tok.cpu().tolist() == ref.tolist()
+    assert tok.cpu().tolist()[:5] == [4092, 100, 4091, 4087, 4088]
+    assert torch.equal(emb.cpu(), table[tok.cpu()])
+
+
 def test_perf_hardening_greedy_routes():
     from mtp_hip import perf_hardening as mh
     g = torch.Generator().manual_seed(10)
