@@ -340,6 +340,30 @@ def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
     assert torch.equal(y, y3)
 
 
+@pytest.mark.parametrize("M,N", [(64, 13000), (48, 16000), (8, 13000), (32, 13000),
+                                 (16, 15000)])
+def test_default_routes_fill_widths(M, N):
+    """The planner's own routes and column widths at N other than 14336
+    (fp8 W, K 4096, gamma and bias): the wave-specialised kernel at 64 / 48
+    rows, the x-resident kernel at 8 / 16 rows, the single-launch kernel at
+    32 rows, each with the width that fills the CUs and a ragged last
+    workgroup; against the oracle."""
+    from mtp_hip import ops
+    K = 4096
+    print(f"case fill width M={M} N={N}", flush=True)
+    g = torch.Generator().manual_seed(M * 13 + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = 0.02 * torch.randn(N, K, generator=g)
+    gm = 1 + 0.1 * torch.randn(K, generator=g)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    wq, ws = O.quantize_fp8_per_channel(W)
+    y = ops.rmsnorm_linear_fp8(_dev(x), _dev(wq), _dev(ws), _dev(b), 1e-6, gamma=_dev(gm))
+    ref = O.rmsnorm_linear_fp8(x, wq, ws, b, 1e-6, gamma=gm)
+    torch.cuda.synchronize()
+    ok, worst = close(y, ref, 2e-2)
+    assert ok, f"worst err/bound = {worst:.3g}"
+
+
 # (columns per workgroup, K-splits, waves, (M, N, K), W kind)
 SKL_TW_CASES = [(224, "4", "8", (32, 3000, 2048), "fp8"), (200, None, "8", (24, 1000, 1024), "fp8"),
                 (64, "2", "4", (40, 300, 512), "same"), (8, None, "8", (7, 100, 256), "fp8"),
