@@ -110,7 +110,7 @@ rmsnorm_vec_kernel(const void *x, const void *r, const void *w, void *y, int N, 
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    if (threadIdx.x + 256 * c >= nch) continue;
+    if ((int)threadIdx.x + 256 * c >= nch) continue;
     unpack16<DT>(xv[c], sv[c]);
     if constexpr (ADD) {
       float t[E];

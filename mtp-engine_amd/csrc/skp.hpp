@@ -74,7 +74,6 @@ skp_kernel(const SkpArgs a) {
   // 10.7 against 11.1; 6 ties 8, 4 loses)
   constexpr int NS = TA == 1 ? 8 : TA == 2 ? 6 : 4;
   static_assert(NS % 2 == 0, "step parity selects the register set");
-  constexpr int BN = 64 * TA;           // columns per workgroup
   constexpr int RB = 2 * UK;            // x bytes of a row per step
   constexpr int RPI = 1024 / RB;        // rows per 1 KB copy instruction
   constexpr int LPR = RB / 16;          // lanes per row in a copy
@@ -100,7 +99,7 @@ skp_kernel(const SkpArgs a) {
   const int b = blockIdx.x;
   int tile, sp;
   split_tile_of(b, a.G, a.S, a.xg != 0, tile, sp);
-  // tw <= BN output columns; the tile's rows past them read zeros and are
+  // tw <= 64 TA output columns; the tile's rows past them read zeros and are
   // not stored
   const int n0 = tile * a.tw;
   const int nend = min(N, n0 + a.tw);
