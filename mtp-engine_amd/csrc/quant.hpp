@@ -115,6 +115,67 @@ fp8_dequantize_kernel(const uint8_t *q, int64_t n, int64_t row_len, const float 
   }
 }
 
+// Per-channel fp8 in one pass: one 256-thread block per row, the row held
+// in registers (NV chunks of 8 elements per thread, all loads issued before
+// the reduction), the block amax, then the row is scaled and written as
+// 8-byte stores. Rows of K = 8 c elements with c <= 256 NV, 16-byte aligned.
+// The same arithmetic as fp8_row_scale_kernel + fp8_quantize_kernel.
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+fp8_rows_vec_kernel(const void *w, int64_t K, uint8_t *q, float *wscale) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t kc = K / 8;
+  float v[NV][8];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = threadIdx.x + 256 * i;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+    if (c < kc) {
+      if constexpr (DT == MTP_F32) {
+        const f32x4 *p = (const f32x4 *)w + 2 * (row * kc + c);
+        const f32x4 a = p[0], b = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[i][e] = a[e];
+          v[i][4 + e] = b[e];
+        }
+      } else {
+        const u32x4 u = ((const u32x4 *)w)[row * kc + c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f32x2 t = unpack2<DT>(u[e]);
+          v[i][2 * e] = t[0];
+          v[i][2 * e + 1] = t[1];
+        }
+      }
+    }
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = amax_acc(m, v[i][e]);
+  m = block_amax_256(m, red);
+  const float s = m > 0.f ? m / 448.0f : 1.0f;
+  if (threadIdx.x == 0) wscale[row] = s;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = threadIdx.x + 256 * i;
+    if (c >= kc) continue;
+    uint32_t b[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      b[e] = f32x2_to_fp8x2(clamp_nan(v[i][2 * e] / s, -448.0f, 448.0f),
+                            clamp_nan(v[i][2 * e + 1] / s, -448.0f, 448.0f));
+    uint2 o;
+    o.x = b[0] | (b[1] << 16);
+    o.y = b[2] | (b[3] << 16);
+    ((uint2 *)q)[row * kc + c] = o;
+  }
+}
+
 // Grouped INT4: one thread per (row, group). scale = amax / 7 (0 -> 1),
 // q = clamp(rint(x / scale), -8, 7), byte k / 2 holds q[k] & 0xF in its low
 // nibble for even k and q[k + 1] & 0xF in its high nibble.
@@ -140,6 +201,69 @@ int4_quantize_kernel(const void *w, int dt, int64_t N, int64_t K, int64_t group,
       hi = ((uint32_t)(int)q1 & 0xFu) << 4;
     }
     packed[row * (K / 2) + k / 2] = (uint8_t)(lo | hi);
+  }
+}
+
+// Grouped INT4, vector form (groups of 8 L elements with L a power of two
+// <= 64, K a multiple of the group, 16-byte aligned rows): lane c takes the
+// 8 consecutive elements of chunk c (one or two 16-byte loads), the L lanes
+// of a group meet by shuffles for the amax, and each lane writes its 4
+// packed bytes. The same arithmetic as int4_quantize_kernel (the maximum of
+// |x| does not depend on the order it is taken in), so the same bytes and
+// scales, from loads that all go out at once.
+template <int DT, int U>
+__global__ void __launch_bounds__(256)
+int4_quantize_vec_kernel(const void *w, int64_t N, int64_t K, int L, uint8_t *packed,
+                         float *scales) {
+  // each wave takes 64 U consecutive chunks, load u at chunk 64 u + lane
+  const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 * U + (threadIdx.x & 63);
+  const int64_t nch = N * K / 8;
+  float v[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t c = c0 + 64 * u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[u][e] = 0.f;
+    if (c < nch) {
+      if constexpr (DT == MTP_F32) {
+        const f32x4 a = ((const f32x4 *)w)[2 * c], b = ((const f32x4 *)w)[2 * c + 1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[u][e] = a[e];
+          v[u][4 + e] = b[e];
+        }
+      } else {
+        const u32x4 q = ((const u32x4 *)w)[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f32x2 t = unpack2<DT>(q[e]);
+          v[u][2 * e] = t[0];
+          v[u][2 * e + 1] = t[1];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = amax_acc(m, v[u][e]);
+    // groups are L consecutive lanes starting at a multiple of L (K / 8 and
+    // 64 are multiples of L), so every lane of a group is in this wave
+    for (int off = 1; off < L; off <<= 1) m = amax_merge(m, __shfl_xor(m, off, 64));
+    const int64_t c = c0 + 64 * u;
+    if (c >= nch) continue;
+    const float s = m > 0.f ? m / 7.0f : 1.0f;
+    // rows hold whole groups, so chunk c is in group c / L of the
+    // row-major [N, K / group] scale matrix
+    if ((c & (L - 1)) == 0) scales[c >> __builtin_ctz(L)] = s;
+    uint32_t out = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q = clamp_nan(rintf(v[u][e] / s), -8.f, 7.f);
+      out |= ((uint32_t)(int)q & 0xFu) << (4 * e);
+    }
+    ((uint32_t *)packed)[c] = out;  // bytes 4 c .. 4 c + 3 = elements 8 c .. 8 c + 7
   }
 }
 

@@ -49,6 +49,27 @@ def test_fp8_per_channel_is_bit_exact():
     assert d["weight_fp8"].dtype == torch.float8_e4m3fn
 
 
+@pytest.mark.parametrize("K", [8, 520, 2056, 4096, 8192, 16384, 522, 16392])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fp8_per_channel_row_widths(K, dtype):
+    """Rows of 8 c elements up to 16384 take the one-pass kernel (1, 2, 4 or
+    8 chunks of 8 per thread); 522 and 16392 take the two-pass kernels. Row
+    0 holds every e4m3 value and every midpoint at scale 1 where it fits."""
+    from mtp_kernels import quantize_fp8_rows
+    g = torch.Generator().manual_seed(K)
+    w = 0.02 * torch.randn(12, K, generator=g)
+    mids = _fp8_midpoints()
+    if K >= mids.numel():
+        w[0] = 0.0
+        w[0, : mids.numel()] = mids
+    w[3] = 0.0
+    w = w.to(dtype)
+    q, s = quantize_fp8_rows(w.to(DEV))
+    qr, sr = O.quantize_fp8_per_channel(w)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+
+
 def test_fp8_dequantize_is_exact():
     from mtp_kernels import dequantize_fp8
     g = torch.Generator().manual_seed(2)
@@ -60,12 +81,16 @@ def test_fp8_dequantize_is_exact():
     assert torch.equal(out, O.dequantize_fp8(qr, sr[:, None]))
 
 
-@pytest.mark.parametrize("group", [32, 128])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_int4_quantize_is_bit_exact_including_ties(group, dtype):
+@pytest.mark.parametrize("group", [8, 32, 128, 512])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", ["whole", "ragged"])
+def test_int4_quantize_is_bit_exact_including_ties(group, dtype, shape):
+    """Whole groups per row take the vector kernel (8 elements per lane, the
+    group's amax by lane shuffles); a ragged last group takes the
+    per-group kernel. Both must give the oracle's bytes and scales."""
     from mtp_kernels import quantize_int4
     g = torch.Generator().manual_seed(group)
-    N, K = 40, 4 * group + 64
+    N, K = 40, 4 * group + (0 if shape == "whole" else 4)
     w = (0.02 * torch.randn(N, K, generator=g)).to(dtype)
     # rows whose groups have amax 7 (scale 1) and half-integer entries
     ties = torch.tensor([-7.5, -6.5, -2.5, -1.5, -0.5, 0.5, 1.5, 2.5, 3.5, 6.5])
