@@ -17,7 +17,9 @@ fraction against its own bound; "verify_step_us" holds the verify steps.
 
 Prints ONE JSON line. The CPU baselines time the oracle's eager
 restatement of the headline workload and of the fp32 configuration on this
-host's cores.
+host's cores; "cpu_context" in "detail" times the same restatement of the
+multi-verify, the tree-verify step and the INT4 linear (whole calls, a
+median of at most three) for context.
 
 `value` and every `us_per_call` are the W warmup + K timed steps the
 command line asks for. A GPU that was idle (each case is built on the CPU
@@ -410,6 +412,57 @@ def cpu_baseline_fp8(torch, M: int):
                        f"{_cpu_model()}")
 
 
+def cpu_context(torch, seconds: float = 8.0):
+    """The oracle's eager restatement of the other workloads, on the host
+    cores, for context: multi-verify (B = 8, depth 4, V = 128256 bf16 head,
+    the B x D loop of logits and argmax), the tree-verify step (64-node
+    attention over 2048 paged tokens, then RMSNorm -> linear 4096 -> 4096)
+    and the INT4 RMSNorm+linear (M = 256, the reference's per-group dequant
+    loop, then fp32 F.linear). Each: one untimed call, then whole calls
+    until `seconds` have passed (at least one, at most three), median."""
+    import math
+    from mtp_hip import workloads
+    from oracle import eager as O
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+
+    def timed(fn):
+        fn()
+        times = []
+        t_end = time.time() + seconds
+        while not times or (time.time() < t_end and len(times) < 3):
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        return round(statistics.median(times) * 1e6, 1), len(times)
+
+    out = {}
+    d = workloads.multi_verify()
+    B, D = d["B"], d["D"]
+    V = d["weight"].shape[0]
+    g = torch.Generator().manual_seed(d["seed"])
+    draft = torch.randint(0, V, (B, D), generator=g, dtype=torch.int32)
+    us, n = timed(lambda: O.fused_multi_verify(d["hidden"], d["weight"], draft))
+    out["multi_verify"] = dict(us_per_call=us, runs=n)
+    del d
+    d = workloads.tree_verify()
+    scale = 1.0 / math.sqrt(d["q"].shape[-1])
+
+    def tree_step():
+        att = O.tree_verify_attention(d["q"], d["k_pages"], d["v_pages"], d["page_table"],
+                                      d["page_size"], d["k_tree"], d["v_tree"], d["tree_mask"],
+                                      scale)
+        return O.rmsnorm_linear(att.reshape(att.shape[0], -1).to(torch.bfloat16), d["weight"],
+                                None, d["eps"], 1.0)
+    us, n = timed(tree_step)
+    out["tree_verify"] = dict(us_per_call=us, runs=n)
+    del d
+    d = workloads.int4_linear()
+    us, n = timed(lambda: O.int4_matmul(d["x"], d["packed"], d["scales"], d["K"], d["group"],
+                                        gamma=d["gamma"], norm=True, eps=d["eps"]))
+    out["int4_M256"] = dict(us_per_call=us, runs=n)
+    return dict(cores=torch.get_num_threads(), kind="port", workloads=out, cpu=_cpu_model())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -500,6 +553,9 @@ def main():
         cpu = cpu_baseline_fp8(torch, 64)
         log("[bench] cpu baseline (oracle, fp32 configuration)")
         detail["cpu_baseline_fp32_M16"] = cpu_baseline_fp32(torch)
+        if not args.only:
+            log("[bench] cpu context (oracle: multi-verify, tree-verify step, INT4)")
+            detail["cpu_context"] = cpu_context(torch)
     verify_us = {k: detail[k]["us_per_call"] for k in ("multi_verify", "multi_verify_bias",
                                                        "multi_verify_fp32", "tree_verify")
                  if k in detail}
