@@ -112,3 +112,26 @@ def test_int4_dequantize_is_exact():
         scales = torch.rand(33, (128 + group - 1) // group, generator=g).to(sdt)
         out = dequantize_int4(packed.to(DEV), scales.to(DEV), 128, group).cpu()
         assert torch.equal(out, O.dequantize_int4(packed, scales, 128, group))
+
+
+def test_quantizers_at_workload_sizes():
+    """The weight producers at the workloads' full sizes, bit for bit: the
+    per-channel fp8 quantizer on the fp8 linear's W [14336, 4096] and the
+    grouped INT4 quantizer (group 128) on the INT4 linear's W [28672,
+    8192], both fp32, both through the vector kernels."""
+    from mtp_kernels import quantize_fp8_rows, quantize_int4
+    g = torch.Generator(device=DEV).manual_seed(11)
+    print("case fp8 rows 14336 x 4096", flush=True)
+    w = 0.02 * torch.randn(14336, 4096, generator=g, device=DEV)
+    q, s = quantize_fp8_rows(w)
+    qr, sr = O.quantize_fp8_per_channel(w.cpu())
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+    del w, q, s, qr, sr
+    print("case int4 28672 x 8192 group 128", flush=True)
+    w = 0.02 * torch.randn(28672, 8192, generator=g, device=DEV)
+    packed, scales = quantize_int4(w, 128)
+    pr, sr = O.quantize_int4(w.cpu(), 128)
+    assert torch.equal(scales.cpu(), sr)
+    assert torch.equal(packed.cpu(), pr)
+
