@@ -61,6 +61,7 @@ enum TuneKey {
   kTuneSkwTw,            // MTP_SKW_TW: its output columns per workgroup (8 .. 64, multiple of 8)
   kTuneSkpTw,            // MTP_SKP_TW: x-resident kernel's columns per workgroup (multiple of 8)
   kTuneSklTw,            // MTP_SKL_TW: single-launch kernel's columns per workgroup (multiple of 8)
+  kTuneSkvR8,            // MTP_SKV_R8: fp32 verify, 8 rows after whole 16-row tiles on the 4x4 MFMA (0: off)
   kTuneCount
 };
 int tune(TuneKey k);

@@ -135,6 +135,12 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 __device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+// 16 independent 4 x 4 x 1 fp32 products: block b = lane / 4 takes A from
+// lanes 4 b .. 4 b + 3 and B from the same lanes; register r of lane l
+// accumulates A[lane 4 b + r] * B[lane l] (layout checked on the device).
+__device__ __forceinline__ f32x4 mfma4_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
 
 // ---- compile-time loops and split waits -------------------------------------
 // f(integral_constant<int, I>) for I = LO .. HI - 1, each a compile-time

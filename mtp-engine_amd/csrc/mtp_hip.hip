@@ -32,7 +32,7 @@ std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
     "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw",
-    "skw", "skw_tw", "skp_tw", "skl_tw"};
+    "skw", "skw_tw", "skp_tw", "skl_tw", "skv_r8"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -70,6 +70,7 @@ void tune_init() {
   g_tune[kTuneSkwTw].store(env_int("MTP_SKW_TW", -1), std::memory_order_relaxed);
   g_tune[kTuneSkpTw].store(env_int("MTP_SKP_TW", -1), std::memory_order_relaxed);
   g_tune[kTuneSklTw].store(env_int("MTP_SKL_TW", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkvR8].store(env_int("MTP_SKV_R8", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -1343,7 +1344,12 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
   const int grid = (int)std::min<int64_t>(ntiles, device_cus());
   for (int64_t m0 = 0; m0 < rows; m0 += rows_per_chunk) {
     const int Mloc = (int)std::min<int64_t>(rows_per_chunk, rows - m0);
-    SkvKernel k = skv_pick(ht, ht == MTP_F32 ? (Mloc + 15) / 16 : (Mloc <= 32 ? 1 : 2));
+    // fp32: 16-row tiles, and 8 rows after whole tiles on the 4 x 4 MFMA
+    // (40 rows: 2 tiles + 8 instead of 3 tiles)
+    const bool r8 = ht == MTP_F32 && Mloc > 16 && Mloc % 16 != 0 && Mloc % 16 <= 8 &&
+                    tune(kTuneSkvR8) != 0;
+    const int mt = ht == MTP_F32 ? (r8 ? Mloc / 16 : (Mloc + 15) / 16) : (Mloc <= 32 ? 1 : 2);
+    SkvKernel k = skv_pick(ht, mt, r8);
     if (!k) return MTP_ERR_DTYPE;
     SkvArgs a{};
     a.x = (const unsigned char *)hidden + m0 * K * dtype_bytes(ht);

@@ -29,6 +29,13 @@
 //     fp32 values of the chunk feed four v_mfma_f32_16x16x4_f32, for 2 W
 //     tiles x MT 16-row x tiles (each MFMA sums k = 4 (4 j + g) + i over the
 //     lane groups g, i fixed; A and B use the same k of every slot).
+//     R8: 8 more rows after the MT 16-row tiles (40 rows = 2 tiles + 8) on
+//     v_mfma_f32_4x4x1_16b_f32, whose 16 blocks are 4 rows x 4 columns x
+//     one k each: A = the 8 rows (lanes 4 b + r: row 4 rg + r, the k of
+//     lane group b / 4), B = the same W registers the 16-row tiles use, so
+//     block b sums one k in four of the step and the four k-groups meet by
+//     two lane shuffles at the end of a tile. Same MFMA rate as the 16-row
+//     tiles on 8 rows instead of 16 padded ones.
 // At the end of a tile each lane adds the bias to its columns and folds
 // them into a running (max, index) per row. At the end the waves' maxima
 // meet in LDS and one lane per row publishes (value, index) as a 64-bit key
@@ -53,8 +60,8 @@ __device__ __forceinline__ float skv_bias_at(__amdgpu_buffer_rsrc_t r, int dt, i
 }
 
 // CT: compute type (BF16, F16, F32); MT: x row tiles (32 rows for 16-bit,
-// 16 rows for fp32).
-template <int CT, int MT>
+// 16 rows for fp32); R8 (fp32): 8 rows after them.
+template <int CT, int MT, bool R8>
 __global__ void __launch_bounds__(512, 1)
 skv_kernel(const SkvArgs a) {
   constexpr bool F32 = CT == MTP_F32;
@@ -62,7 +69,8 @@ skv_kernel(const SkvArgs a) {
   constexpr int TR = F32 ? 16 : 32;          // rows per x tile
   constexpr int KS = F32 ? 2 : 4;            // compute steps per stage
   constexpr int WST = BN * kSkUB;            // W bytes of one stage (32 KB)
-  constexpr int XST = MT * TR * kSkUB;       // x bytes of one stage
+  constexpr int XR = MT * TR + (R8 ? 8 : 0);  // x rows
+  constexpr int XST = XR * kSkUB;            // x bytes of one stage
   constexpr int NS = 4;                      // register ring stages (loads run NS - 1 ahead)
   constexpr int NWC = WST / 1024 / 8;        // W loads per wave per stage (4)
   constexpr int NXC = (XST / 1024 + 7) / 8;  // x loads per wave per stage (<= 1)
@@ -70,7 +78,8 @@ skv_kernel(const SkvArgs a) {
   constexpr int NQ = F32 ? 8 : 16;           // columns per lane per tile
   static_assert(NXC == 1, "one x block per wave and stage at most");
   static_assert((NS - 1) * NV < 64, "vmcnt is 6 bits");
-  static_assert(MT * TR <= 64, "at most 64 rows");
+  static_assert(XR <= 64, "at most 64 rows");
+  static_assert(!R8 || F32, "the 8-row remainder is an fp32 form");
   __shared__ __attribute__((aligned(1024))) unsigned char lds_w[2 * WST];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_x[2 * XST];
   __shared__ unsigned long long s_key[8][64];
@@ -147,7 +156,17 @@ skv_kernel(const SkvArgs a) {
   // fp32: acc4[u][t] of W tile u (16 columns) x x tile t (16 rows)
   f32x16 acc[F32 ? 1 : MT];
   f32x4 acc4[2][F32 ? MT : 1];
+  // R8: accR[u][rg] of W tile u x rows MT * 16 + 4 rg .. + 3, per k-group
+  f32x4 accR[2][2];
   auto zero_acc = [&]() __attribute__((always_inline)) {
+    if constexpr (R8) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) accR[u][rg][e] = 0.f;
+    }
     if constexpr (F32) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -194,14 +213,31 @@ skv_kernel(const SkvArgs a) {
           const int row = 16 * t + (lane & 15);
           bv[t] = *(const u32x4 *)(xb + row * kSkUB + ((c ^ sk_swz(row)) << 4));
         }
+        u32x4 bx[2];
+        if constexpr (R8) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int rg = 0; rg < 2; ++rg) {
+            const int row = 16 * MT + 4 * rg + (lane & 3);
+            bx[rg] = *(const u32x4 *)(xb + row * kSkUB + ((c ^ sk_swz(row)) << 4));
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
           for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int t = 0; t < MT; ++t)
               acc4[u][t] = mfma16_f32(__uint_as_float(av[u][i]), __uint_as_float(bv[t][i]),
                                       acc4[u][t]);
+          if constexpr (R8) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+              for (int rg = 0; rg < 2; ++rg)
+                accR[u][rg] = mfma4_f32(__uint_as_float(bx[rg][i]), __uint_as_float(av[u][i]),
+                                        accR[u][rg]);
+          }
+        }
       } else {
         const int row = 32 * wave + (lane & 31);
         const int c = 2 * j + ag;
@@ -230,13 +266,21 @@ skv_kernel(const SkvArgs a) {
   const __amdgpu_buffer_rsrc_t brs =
       make_rsrc(a.bias, has_bias ? (uint32_t)N * (uint32_t)dtype_bytes(a.bias_dt) : 0u);
   float bias_v[NQ];
+  // R8: the lane's remainder columns are 32 wave + 16 u + lane % 16
+  float bias_r[2];
   auto load_bias = [&](int tile) __attribute__((always_inline)) {
     if (has_bias) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) bias_v[q] = skv_bias_at(brs, a.bias_dt, tile * BN + col_of(q));
+      if constexpr (R8) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          bias_r[u] = skv_bias_at(brs, a.bias_dt, tile * BN + 32 * wave + 16 * u + (lane & 15));
+      }
     } else {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) bias_v[q] = 0.f;
+      bias_r[0] = bias_r[1] = 0.f;
     }
   };
 
@@ -248,7 +292,41 @@ skv_kernel(const SkvArgs a) {
     best_v[t] = -__builtin_inff();
     best_n[t] = 0x7fffffff;
   }
+  // R8: row MT * 16 + 4 rg + r over the lane's remainder columns
+  float bestr_v[2][4];
+  int bestr_n[2][4];
+#pragma unroll
+  for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      bestr_v[rg][r] = -__builtin_inff();
+      bestr_n[rg][r] = 0x7fffffff;
+    }
   auto end_tile = [&](int tile) __attribute__((always_inline)) {
+    if constexpr (R8) {
+      // the four k-groups of a block (lanes l, l ^ 16, l ^ 32, l ^ 48) sum
+      // in the same order on every lane; register r of lane l is then row
+      // MT * 16 + 4 rg + r, column 32 wave + 16 u + l % 16
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          f32x4 v = accR[u][rg];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += __shfl_xor(v[e], 16, 64);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += __shfl_xor(v[e], 32, 64);
+          const int n = tile * BN + 32 * wave + 16 * u + (lane & 15);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = v[r] + bias_r[u];
+            if (n < N && argmax_better(x, n, bestr_v[rg][r], bestr_n[rg][r])) {
+              bestr_v[rg][r] = x;
+              bestr_n[rg][r] = n;
+            }
+          }
+        }
+    }
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -319,6 +397,27 @@ skv_kernel(const SkvArgs a) {
     if (lane < TR)
       s_key[wave][TR * t + lane] =
           best_n[t] == 0x7fffffff ? 0ull : argmax_key(best_v[t], best_n[t]);
+  }
+  if constexpr (R8) {
+    // the 16 column lanes of each remainder row (the other lane groups hold
+    // the same values)
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int sh = 1; sh < 16; sh *= 2) {
+          const float ov = __shfl_xor(bestr_v[rg][r], sh, 64);
+          const int on = __shfl_xor(bestr_n[rg][r], sh, 64);
+          if (argmax_better(ov, on, bestr_v[rg][r], bestr_n[rg][r])) {
+            bestr_v[rg][r] = ov;
+            bestr_n[rg][r] = on;
+          }
+        }
+        if (lane == 0)
+          s_key[wave][16 * MT + 4 * rg + r] =
+              bestr_n[rg][r] == 0x7fffffff ? 0ull : argmax_key(bestr_v[rg][r], bestr_n[rg][r]);
+      }
   }
   __syncthreads();
   if (th < a.M) {

@@ -32,6 +32,8 @@ struct SkvArgs {
 typedef void (*SkvKernel)(SkvArgs);
 // Kernel for compute type ct and mt row tiles: BF16 / F16 with 1-2 tiles of
 // 32 rows, F32 with 1-4 tiles of 16 rows; null otherwise.
-SkvKernel skv_pick(int ct, int mt);
+// mt: 32-row (16-bit) or 16-row (fp32) x tiles; r8 (fp32, mt 1..3): 8 rows
+// after them.
+SkvKernel skv_pick(int ct, int mt, bool r8);
 
 }  // namespace mtp

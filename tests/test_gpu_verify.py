@@ -129,6 +129,31 @@ def test_multi_verify_matches_oracle(dtype, B, D, K, V, bias):
     _check_chain(out, hidden, W, b, draft, 1e-3)
 
 
+@pytest.mark.parametrize("B,D", [(8, 4), (6, 3), (14, 3), (10, 1), (9, 1)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_fp32_verify_eight_row_remainder(B, D, bias, tune):
+    """fp32 rows past whole 16-row tiles (40 = 2 x 16 + 8, 24, 56, 20 and
+    18: 4 and 6 padding rows) on the 4 x 4 MFMA form of the streaming
+    kernel, against the oracle, and against the padded form (tuning key
+    skv_r8 = 0) wherever the top-2 gap is clear."""
+    from mtp_hip import ops
+    K, V = 256, 20000
+    hidden, W, b, draft, top, gap = _chain_case(B, D, K, V, torch.float32, seed=B * 17 + D,
+                                                bias=bias)
+    hd, Wd, dd = hidden.to(DEV), W.to(DEV), draft.to(DEV)
+    bd = None if b is None else b.to(DEV)
+    assert ops.verify_route(hd, Wd, bd) == "stream"
+    print(f"case fp32 remainder B={B} D={D} bias={bias}", flush=True)
+    out = ops.multi_verify(hd, Wd, dd, bd, return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hidden, W, b, draft, 1e-3)
+    tune(skv_r8=0)
+    pad = ops.multi_verify(hd, Wd, dd, bd, return_top=True)
+    torch.cuda.synchronize()
+    sure = (gap > 1e-3).reshape(-1)
+    assert torch.equal(out[3].cpu().reshape(-1)[sure], pad[3].cpu().reshape(-1)[sure])
+
+
 def test_workspace_shared_across_kernels_and_shapes():
     """Split-K linear, verify and multi-verify calls of different shapes share
     one per-stream workspace; each must still match the oracle (the arrival
