@@ -400,6 +400,18 @@ int fill_width(int64_t N, int S, int full) {
   const int64_t w = (per + 7) / 8 * 8;
   return (w < full && 4 * w >= 3 * (int64_t)full) ? (int)w : full;
 }
+// Columns per workgroup (a multiple of 8, at most `full`) that split N S
+// columns into whole rounds of one workgroup per CU: the fewest rounds R
+// whose width ceil(N S / (CUs R)) fits, so the grid ends within 8 columns
+// per workgroup of a whole round (a partial last round of a few workgroups
+// costs about as much as a full one).
+int round_width(int64_t N, int S, int full) {
+  const int64_t cus = device_cus();
+  for (int64_t R = 1;; ++R) {
+    const int64_t w = ((N * S + cus * R - 1) / (cus * R) + 7) / 8 * 8;
+    if (w <= full) return (int)w;
+  }
+}
 constexpr int kSkMinStages = 4;    // stages per split at least
 
 // Tile: 64 columns x all rows of x (<= 64); K-splits only while the grid is
@@ -622,7 +634,15 @@ PlanSkl make_plan_skl(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
     if (t > bn || t % 8 != 0) return p;
     p.tw = t;
   } else {
-    p.tw = fill_width(N, p.S, (int)bn);
+    // wide N without K-splits (a 64-column tile per CU at least): whole
+    // rounds of one workgroup per CU where that narrows the tile by at most
+    // half (bf16 8 x 151936 x 4096: 200 columns, 760 workgroups, 183.3
+    // against 198.4 µs with 256 columns in 594 workgroups); otherwise one
+    // round filled
+    const int rw = p.S == 1 ? round_width(N, 1, (int)bn) : 0;
+    p.tw = p.S == 1 && 2 * rw >= (int)bn && N >= (int64_t)device_cus() * 64
+               ? rw
+               : fill_width(N, p.S, (int)bn);
   }
   p.G = (int)((N + p.tw - 1) / p.tw);
   if ((int64_t)p.G * p.S > INT32_MAX) return p;
@@ -727,9 +747,20 @@ PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
   if (S > p.nkb) S = p.nkb;
   p.kb_per = (p.nkb + S - 1) / S;
   p.S = (p.nkb + p.kb_per - 1) / p.kb_per;
+  // wide N without K-splits (at least a 64-column tile per CU): the width
+  // that splits the columns into whole rounds of one workgroup per CU, on
+  // the narrowest tile (1, 2 or 4 A tiles per wave) that holds it; bf16 K
+  // 4096, 8 rows, µs per call: N 40960 53.7 against 62.5 (128-column
+  // tiles, 320 workgroups), N 151936 186.4 against 200.5 (256 columns, 594
+  // workgroups)
+  const bool wide = tune(kTuneSkpTa) <= 0 && tune(kTuneSkpTw) <= 0 && p.S == 1 &&
+                    N >= (int64_t)device_cus() * 64;
+  const int rw = wide ? round_width(N, 1, 256) : 0;
   if (tune(kTuneSkpTa) > 0) {
     const int t = tune(kTuneSkpTa);
     p.ta = t >= 4 ? 4 : t >= 2 ? 2 : 1;
+  } else if (wide) {
+    p.ta = rw <= 64 ? 1 : rw <= 128 ? 2 : 4;
   } else {
     p.ta = 1;
     for (int t = 4; t >= 2; t /= 2)
@@ -745,6 +776,8 @@ PlanSkp make_plan_skp(int ct, int wt, int64_t M, int64_t N, int64_t K, bool gam)
     const int t = tune(kTuneSkpTw);
     if (t > 64 * p.ta || t % 8 != 0) return p;
     p.tw = t;
+  } else if (wide) {
+    p.tw = rw;
   } else {
     p.tw = fill_width(N, p.S, 64 * p.ta);
   }
@@ -862,12 +895,23 @@ int rmsnorm_linear_impl(const void *x, int xt, int64_t M, int64_t K, const void 
   const int skpm = skp_mode();
   if (skpm != 0 && aligned && (!gamma || gt == MTP_F32)) {
     const PlanSkp pp = make_plan_skp(xt, wt, M, N, K, gamma != nullptr);
+    // past N = 32768 with at least 48 MiB of W the single-launch kernel
+    // streams W faster for these rows too (K 4096, 8 rows, µs per call:
+    // bf16 N 40960 51.9 against 53.5, N 128256 155.1 against 157.0, fp8 N
+    // 65536 46.6 against 47.4; at N 32768 and below the x-resident kernel
+    // leads: bf16 42.7 against 57.4)
+    bool to_skl = false;
+    if (tune(kTuneSkp) != 1 && N > 32768 && skl_mode() != 0 &&
+        N * K * dtype_bytes(wt) >= kSklSplitMinWBytes) {
+      const PlanSkl pl = make_plan_skl(xt, wt, M, N, K, gamma != nullptr);
+      to_skl = pl.ok;
+    }
     // by default up to 16 rows (one x tile); above that the split-K
     // hand-off and the per-workgroup in-place pass cost more than the other
     // kernels' x re-reads (fp8 K 4096 N 14336: 8 rows 14.5 us vs 18.0,
     // 16 rows 16.4 vs 18.4, 32 rows 20.8 vs 19.9, 64 rows 31 vs 24; 16-bit W
     // 4096 x 4096, 16 rows: 11.1 vs 14.3)
-    if (pp.ok && (tune(kTuneSkp) == 1 || pp.mt == 1)) {
+    if (pp.ok && !to_skl && (tune(kTuneSkp) == 1 || pp.mt == 1)) {
       if (!ws || ws_bytes < pp.total) return MTP_ERR_WORKSPACE;
       SkpArgs pa{};
       pa.x = x;

@@ -341,13 +341,15 @@ def test_single_launch_skinny_kernel(splits, waves, shape, wkind, xdtype):
 
 
 @pytest.mark.parametrize("M,N", [(64, 13000), (48, 16000), (8, 13000), (32, 13000),
-                                 (16, 15000)])
+                                 (16, 15000), (8, 40960), (4, 50257)])
 def test_default_routes_fill_widths(M, N):
     """The planner's own routes and column widths at N other than 14336
     (fp8 W, K 4096, gamma and bias): the wave-specialised kernel at 64 / 48
     rows, the x-resident kernel at 8 / 16 rows, the single-launch kernel at
     32 rows, each with the width that fills the CUs and a ragged last
-    workgroup; against the oracle."""
+    workgroup; 8 and 4 rows at N past 32768 on the single-launch kernel
+    with the widths that make whole rounds (160 and 200 columns); against
+    the oracle."""
     from mtp_hip import ops
     K = 4096
     print(f"case fill width M={M} N={N}", flush=True)
@@ -472,7 +474,8 @@ def test_x_resident_skinny_kernel(splits, ta, h8, shape, wkind, xdtype):
 # (columns per workgroup, K-splits, A tiles per wave, (M, N, K), W kind)
 SKP_TW_CASES = [(56, None, None, (8, 1000, 4096), "fp8"), (40, "2", None, (5, 300, 1024), "fp8"),
                 (8, None, None, (16, 57, 512), "same"), (112, None, "2", (9, 700, 2048), "fp8"),
-                (48, "3", "1", (33, 260, 1536), "fp8"), (24, None, None, (2, 100, 256), "same")]
+                (48, "3", "1", (33, 260, 1536), "fp8"), (24, None, None, (2, 100, 256), "same"),
+                (160, None, "4", (8, 1000, 1024), "same"), (200, "2", "4", (3, 1500, 2048), "fp8")]
 
 
 @pytest.mark.parametrize("tw,splits,ta,shape,wkind", SKP_TW_CASES)
