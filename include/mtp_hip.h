@@ -92,12 +92,14 @@ const char *mtp_last_hip_error(void);
  * tile width; default: narrowed by at most a quarter so that the grid puts
  * one workgroup on every CU), "skv_r8" (0: the fp32 verify pads 8 rows
  * past whole 16-row tiles to a full tile instead of running them on the
- * 4 x 4 MFMA). value -1
+ * 4 x 4 MFMA), "skv_tw" (columns per tile of the streaming verify, a
+ * multiple of 8 up to 256; default: whole rounds of one tile per CU from
+ * a 64-column tile per CU). value -1
  * restores the planner's choice. The MTP_SKL, MTP_SK_SPLITS, MTP_WS_TUNE
  * ("variant,splits"), MTP_SKL_WAVES, MTP_SKL_SPLITS, MTP_ATTN_CHUNK_BLOCKS,
  * MTP_INT4_WAVES, MTP_VERIFY_WSTREAM, MTP_SKP, MTP_SKP_SPLITS, MTP_SKP_TA,
- * MTP_SKP_H8, MTP_SF32, MTP_ATTN32, MTP_SK_XRAW, MTP_SKW, MTP_SKW_TW, MTP_SKP_TW, MTP_SKL_TW and
- * MTP_SKV_R8 environment variables
+ * MTP_SKP_H8, MTP_SF32, MTP_ATTN32, MTP_SK_XRAW, MTP_SKW, MTP_SKW_TW, MTP_SKP_TW, MTP_SKL_TW,
+ * MTP_SKV_R8 and MTP_SKV_TW environment variables
  * seed the keys once, at the
  * first launch plan. MTP_ERR_ARG for an unknown key.
  */

@@ -62,6 +62,7 @@ enum TuneKey {
   kTuneSkpTw,            // MTP_SKP_TW: x-resident kernel's columns per workgroup (multiple of 8)
   kTuneSklTw,            // MTP_SKL_TW: single-launch kernel's columns per workgroup (multiple of 8)
   kTuneSkvR8,            // MTP_SKV_R8: fp32 verify, 8 rows after whole 16-row tiles on the 4x4 MFMA (0: off)
+  kTuneSkvTw,            // MTP_SKV_TW: streaming verify's columns per tile (8 .. 256, multiple of 8)
   kTuneCount
 };
 int tune(TuneKey k);

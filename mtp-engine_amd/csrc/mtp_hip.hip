@@ -32,7 +32,7 @@ std::once_flag g_tune_once;
 const char *const kTuneNames[kTuneCount] = {
     "skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
     "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits", "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw",
-    "skw", "skw_tw", "skp_tw", "skl_tw", "skv_r8"};
+    "skw", "skw_tw", "skp_tw", "skl_tw", "skv_r8", "skv_tw"};
 
 int env_int(const char *name, int dflt) {
   const char *e = std::getenv(name);
@@ -71,6 +71,7 @@ void tune_init() {
   g_tune[kTuneSkpTw].store(env_int("MTP_SKP_TW", -1), std::memory_order_relaxed);
   g_tune[kTuneSklTw].store(env_int("MTP_SKL_TW", -1), std::memory_order_relaxed);
   g_tune[kTuneSkvR8].store(env_int("MTP_SKV_R8", -1), std::memory_order_relaxed);
+  g_tune[kTuneSkvTw].store(env_int("MTP_SKV_TW", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -1384,7 +1385,19 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
   if (!aligned16(hidden) || !aligned16(w)) return MTP_ERR_ALIGN;
   if (!ws || ws_bytes < kCounterBytes) return MTP_ERR_WORKSPACE;
   unsigned char *w8 = (unsigned char *)ws;
-  const int64_t ntiles = (V + kSkvBN - 1) / kSkvBN;
+  // columns per tile: from a 64-column tile per CU, the width that makes
+  // whole rounds of one tile per CU (V 32000: 128 columns, 250 workgroups
+  // instead of 125; V 151936: 200 columns, 760 tiles in three rounds
+  // instead of 594 in two and a third); tuning key skv_tw sets it
+  int tw = kSkvBN;
+  if (tune(kTuneSkvTw) > 0) {
+    tw = std::min(kSkvBN, tune(kTuneSkvTw) / 8 * 8);
+    if (tw < 8) return MTP_ERR_ARG;
+  } else if (V >= (int64_t)device_cus() * 64) {
+    tw = round_width(V, 1, kSkvBN);
+  }
+  const int64_t ntiles = (V + tw - 1) / tw;
+  if (ntiles > INT32_MAX) return MTP_ERR_SHAPE;
   const int grid = (int)std::min<int64_t>(ntiles, device_cus());
   for (int64_t m0 = 0; m0 < rows; m0 += rows_per_chunk) {
     const int Mloc = (int)std::min<int64_t>(rows_per_chunk, rows - m0);
@@ -1404,6 +1417,7 @@ static int launch_skv(const void *hidden, int ht, int64_t rows, int64_t K, const
     a.N = (int)V;
     a.K = (int)K;
     a.ntiles = (int)ntiles;
+    a.tw = tw;
     a.nst = (int)(K * dtype_bytes(ht) / kSkUB);  // 128-byte stages of a W row
     a.keys = (unsigned long long *)(w8 + kSkvKeysOff);
     a.ticket = (unsigned *)w8;

@@ -7,7 +7,10 @@
 //                                                wins ties)
 //
 // One launch of one workgroup per CU streams W once.
-// Workgroup b takes the kSkvBN-column tiles b, b + grid, b + 2 grid, ...
+// Workgroup b takes the tw-column tiles b, b + grid, b + 2 grid, ... (tw
+// <= kSkvBN: the host narrows the 256-column MFMA tile so that the tiles
+// make whole rounds of one workgroup per CU; columns past tw read zeros
+// and never enter the argmax)
 // back to back; the stages (128 bytes of every W row of a tile: 64 k of
 // 16-bit W, 32 k of fp32 W) of all its tiles form one sequence, so the
 // register rings run across tile boundaries without draining; each tile's
@@ -99,10 +102,12 @@ skv_kernel(const SkvArgs a) {
   const int rot = (7 * b) % nst;
 
   const uint32_t ldw = (uint32_t)a.K * (uint32_t)dtype_bytes(CT);
-  // W of tile t: rows t * BN .. t * BN + BN - 1 (rows past N read zeros)
+  // W of tile t: rows t * tw .. t * tw + tw - 1 (rows past them, or past N,
+  // read zeros)
+  const int tw = a.tw;
   auto w_rsrc = [&](int tile) __attribute__((always_inline)) {
-    const int rows = min(BN, N - tile * BN);
-    return make_rsrc((const unsigned char *)a.w + (size_t)tile * BN * ldw, (uint32_t)rows * ldw);
+    const int rows = min(tw, N - tile * tw);
+    return make_rsrc((const unsigned char *)a.w + (size_t)tile * tw * ldw, (uint32_t)rows * ldw);
   };
   // W load c (c = wave + 8 i): rows 8 c .. 8 c + 7 of the tile, lane l: row
   // 8 c + l / 8, 16-byte chunk (l % 8) ^ sk_swz(row) of the stage's 128 bytes
@@ -271,11 +276,11 @@ skv_kernel(const SkvArgs a) {
   auto load_bias = [&](int tile) __attribute__((always_inline)) {
     if (has_bias) {
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) bias_v[q] = skv_bias_at(brs, a.bias_dt, tile * BN + col_of(q));
+      for (int q = 0; q < NQ; ++q) bias_v[q] = skv_bias_at(brs, a.bias_dt, tile * tw + col_of(q));
       if constexpr (R8) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-          bias_r[u] = skv_bias_at(brs, a.bias_dt, tile * BN + 32 * wave + 16 * u + (lane & 15));
+          bias_r[u] = skv_bias_at(brs, a.bias_dt, tile * tw + 32 * wave + 16 * u + (lane & 15));
       }
     } else {
 #pragma unroll
@@ -316,11 +321,11 @@ skv_kernel(const SkvArgs a) {
           for (int e = 0; e < 4; ++e) v[e] += __shfl_xor(v[e], 16, 64);
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] += __shfl_xor(v[e], 32, 64);
-          const int n = tile * BN + 32 * wave + 16 * u + (lane & 15);
+          const int cn = 32 * wave + 16 * u + (lane & 15), n = tile * tw + cn;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float x = v[r] + bias_r[u];
-            if (n < N && argmax_better(x, n, bestr_v[rg][r], bestr_n[rg][r])) {
+            if (cn < tw && n < N && argmax_better(x, n, bestr_v[rg][r], bestr_n[rg][r])) {
               bestr_v[rg][r] = x;
               bestr_n[rg][r] = n;
             }
@@ -331,9 +336,9 @@ skv_kernel(const SkvArgs a) {
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        const int n = tile * BN + col_of(q);
+        const int n = tile * tw + col_of(q);
         const float v = (F32 ? acc4[q >> 2][t][q & 3] : acc[t][q]) + bias_v[q];
-        if (n < N && argmax_better(v, n, best_v[t], best_n[t])) {
+        if (col_of(q) < tw && n < N && argmax_better(v, n, best_v[t], best_n[t])) {
           best_v[t] = v;
           best_n[t] = n;
         }

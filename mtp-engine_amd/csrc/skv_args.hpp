@@ -15,7 +15,8 @@ struct SkvArgs {
   const void *bias;     // [N] bias_dt (F32 / BF16 / F16) or null
   int bias_dt;
   int M, N, K;          // M <= 64
-  int ntiles, nst;      // kSkvBN-column tiles, stages (64 k) per tile
+  int ntiles, nst;      // column tiles, stages (128 bytes of a W row) per tile
+  int tw;               // columns per tile (a multiple of 8, at most kSkvBN)
   unsigned long long *keys;  // [64] packed (value, index) maxima, zero between launches
   unsigned *ticket;          // arrival ticket, zero between launches
   // outputs (already offset to this chunk's rows / batch elements)

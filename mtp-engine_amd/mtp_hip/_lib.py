@@ -155,7 +155,7 @@ def check(status: int, what: str) -> None:
 TUNING_KEYS = ("skl", "sk_splits", "ws_variant", "ws_splits", "skl_waves", "skl_splits",
                "attn_chunk_blocks", "int4_waves", "verify_wstream", "skp", "skp_splits",
                "skp_ta", "sf32", "skp_h8", "attn32", "sk_xraw",
-               "skw", "skw_tw", "skp_tw", "skl_tw", "skv_r8")
+               "skw", "skw_tw", "skp_tw", "skl_tw", "skv_r8", "skv_tw")
 
 
 def set_tuning(**keys: int) -> None:

@@ -154,6 +154,25 @@ def test_fp32_verify_eight_row_remainder(B, D, bias, tune):
     assert torch.equal(out[3].cpu().reshape(-1)[sure], pad[3].cpu().reshape(-1)[sure])
 
 
+@pytest.mark.parametrize("tw", [8, 40, 200, 256])
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 20000), (torch.float32, 3001)])
+def test_streaming_verify_tile_widths(tw, dtype, V, tune):
+    """The streaming verify kernel with tw columns per tile (tuning key
+    skv_tw; columns past tw read zeros and stay out of the argmax), a bias
+    and a ragged last tile: against the oracle wherever the top-2 gap is
+    clear."""
+    from mtp_hip import ops
+    B, D, K = 6, 4, 256
+    hidden, W, b, draft, top, gap = _chain_case(B, D, K, V, dtype, seed=tw + V, bias=True)
+    hd, Wd, dd, bd = hidden.to(DEV), W.to(DEV), draft.to(DEV), b.to(DEV)
+    assert ops.verify_route(hd, Wd, bd) == "stream"
+    tune(skv_tw=tw)
+    print(f"case skv tw={tw} dtype={dtype} V={V}", flush=True)
+    out = ops.multi_verify(hd, Wd, dd, bd, return_top=True)
+    torch.cuda.synchronize()
+    _check_chain(out, hidden, W, b, draft, 1e-3)
+
+
 def test_workspace_shared_across_kernels_and_shapes():
     """Split-K linear, verify and multi-verify calls of different shapes share
     one per-stream workspace; each must still match the oracle (the arrival
